@@ -1,0 +1,218 @@
+/*
+ * nflow_quant.h -- C-ABI of the MI355X (gfx950) quantised inference GEMM.
+ *
+ * This library replaces NeuroFlow's CPU INT8 GEMM (`nflow::int8_gemm`,
+ * cpp/include/neuroflow/int8_gemm.h) and FP8 E4M3 codec
+ * (cpp/include/neuroflow/fp8_e4m3.h) with hand-written HIP kernels.  Every
+ * entry point is `extern "C"`, takes plain pointers and sizes, and returns a
+ * status code with the values of `nflow::StatusCode`
+ * (cpp/include/neuroflow/tensor.h:29-37).  The message of the last failing
+ * call on the calling thread is available from nflow_last_error().
+ *
+ * Memory: every array argument of a device entry point is a DEVICE pointer
+ * (hipMalloc'd, or a torch CUDA tensor's data_ptr()), unless the function
+ * name starts with nflow_host_.  Kernels are enqueued on `stream` (a
+ * hipStream_t; NULL = the default stream) and the call returns without
+ * synchronising; results are ready once the stream has been synchronised.
+ * Calls on one stream execute in order; the library keeps no state between
+ * calls except a cached device-property lookup.
+ *
+ * Numerics (the reference's x86 build is the specification):
+ *   - activation codes: clamp(int32(roundf(a / scale)) + zp, -128, 127) with a
+ *     correctly rounded division, half-away-from-zero rounding, and the x86
+ *     conversion result INT32_MIN for NaN / |q| >= 2^31;
+ *   - int32 accumulators are exact;
+ *   - dequantise: (scale_W[o] * scale_A) * float(acc) + bias[o], no FMA;
+ *   - FP8 E4M3 bytes reproduce fp32_to_e4m3_bits bit for bit;
+ *   - GELU is the tanh form of fno.cpp:41-46.
+ */
+#ifndef NFLOW_QUANT_H
+#define NFLOW_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NFLOW_QUANT_ABI_VERSION 1
+
+/* nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37. */
+enum nflow_status_code {
+    NFLOW_OK = 0,
+    NFLOW_INVALID_ARG = 1,
+    NFLOW_FILE_NOT_FOUND = 2,
+    NFLOW_PARSE_ERROR = 3,
+    NFLOW_SHAPE_MISMATCH = 4,
+    NFLOW_UNSUPPORTED_OP = 5,
+    NFLOW_INTERNAL = 99
+};
+
+/* Epilogue activation (ApplyActivation, cpp/src/fno.cpp:36-48). */
+enum nflow_activation {
+    NFLOW_ACT_NONE = 0,
+    NFLOW_ACT_RELU = 1,
+    NFLOW_ACT_GELU_TANH = 2
+};
+
+/* nflow::int8_gemm::Int8LinearParams (cpp/include/neuroflow/int8_gemm.h:45-65),
+ * field for field, with device pointers. */
+typedef struct nflow_int8_linear_params {
+    const int8_t* W_int8;         /* (out_features, in_features) row-major */
+    const float* scale_W;         /* (out_features) per-channel scale */
+    const int32_t* zp_W;          /* (out_features) per-channel zero point */
+    const float* bias;            /* (out_features) or NULL */
+    int in_features;
+    int out_features;
+    float scale_A;                /* per-tensor activation scale */
+    int32_t zp_A;                 /* per-tensor activation zero point */
+    const int32_t* sum_W_per_row; /* (out_features) or NULL */
+} nflow_int8_linear_params;
+
+/* FP8 E4M3 layer: per-channel symmetric weights (bytes as produced by
+ * fp32_to_e4m3_bits, fp8_e4m3.h:106-215), no zero points. */
+typedef struct nflow_fp8_linear_params {
+    const uint8_t* W_e4m3;        /* (out_features, in_features) row-major */
+    const float* scale_W;         /* (out_features) */
+    const float* bias;            /* (out_features) or NULL */
+    int in_features;
+    int out_features;
+} nflow_fp8_linear_params;
+
+/* ---- library ------------------------------------------------------------ */
+
+int nflow_quant_abi_version(void);
+
+/* Message of the last non-OK status returned on this thread ("" if none). */
+const char* nflow_last_error(void);
+
+/* ---- nflow-quant kernel API (cpp/include/neuroflow/int8_gemm.h) ------------ */
+
+/* Replaces int8_gemm::QuantiseActivation (int8_gemm.h:115-118,
+ * int8_gemm.cpp:507-520).  A (bsz, in_features) fp32 -> A_q int8.  Null A or
+ * A_q is a silent no-op returning NFLOW_OK, as the reference returns void. */
+int nflow_int8_quantise_activation(const float* A, int8_t* A_q, int64_t bsz,
+                                   int in_features, float scale_A, int32_t zp_A,
+                                   void* stream);
+
+/* Replaces int8_gemm::PrecomputeSumW (int8_gemm.h:74-76,
+ * int8_gemm.cpp:479-496): sum_W_out[o] = sum_i (W_int8[o,i] - zp_W[o]).
+ * The result goes to caller-owned device memory instead of a new[] array;
+ * where the reference returns nullptr (null input, dims <= 0) this returns
+ * NFLOW_INVALID_ARG. */
+int nflow_int8_precompute_sum_w(const int8_t* W_int8, const int32_t* zp_W,
+                                int in_features, int out_features,
+                                int32_t* sum_W_out, void* stream);
+
+/* Replaces int8_gemm::LinearForward (int8_gemm.h:90-91,
+ * int8_gemm.cpp:201-470) as built with the reference's AVX-512 VNNI flags:
+ * one activation row A (in_features) -> C (out_features).  Errors as the
+ * reference: null W_int8/scale_W/zp_W/A/C or dims <= 0 -> NFLOW_INVALID_ARG. */
+int nflow_int8_linear_forward(const nflow_int8_linear_params* p, const float* A,
+                              float* C, void* stream);
+
+/* LinearForward applied to each of `rows` rows of A with the same params
+ * (the reference's per-row calling pattern, fno.cpp:87-110), in one launch. */
+int nflow_int8_linear_forward_rows(const nflow_int8_linear_params* p, int64_t rows,
+                                   const float* A, float* C, void* stream);
+
+/* Replaces int8_gemm::LinearForwardBatched (int8_gemm.h:102-104,
+ * int8_gemm.cpp:530-580).  bsz <= 0 -> NFLOW_OK with no work; null A or C ->
+ * NFLOW_INVALID_ARG (the reference also dereferences W_int8/scale_W/zp_W
+ * unchecked: here those are NFLOW_INVALID_ARG as well). */
+int nflow_int8_linear_forward_batched(const nflow_int8_linear_params* p, int64_t bsz,
+                                      const float* A, float* C, void* stream);
+
+/* ---- per-token (dynamic) INT8 path ------------------------------------------
+ * The reference's per-token path is LinearForward called once per row with
+ * that row's scale_A (bench_int8_gemm.cpp:163, fno.cpp:87-110).  Here the
+ * per-row scale is computed on the device: scale_A[m] = absmax(row m) / 127
+ * (1.0f for an all-zero row), zp_A = 0. */
+
+/* A (M, K) fp32 -> A_q (M, K) int8 codes, scale_A (M), optional sum_a (M) =
+ * sum of each row's codes. */
+int nflow_int8_quantise_per_token(const float* A, int64_t M, int K, int8_t* A_q,
+                                  float* scale_A, int32_t* sum_a, void* stream);
+
+/* The fused hot path: per-token quantise -> INT8 MFMA GEMM -> dequantise +
+ * bias + activation, i.e. for every row m the result of LinearForward(p with
+ * scale_A = absmax(row m)/127, zp_A = 0) followed by `activation`.  p->scale_A
+ * and p->zp_A are ignored.  scale_A_out (nullable, M floats) receives the
+ * per-row scales. */
+int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64_t M,
+                                        const float* A, float* C, float* scale_A_out,
+                                        int activation, void* stream);
+
+/* Raw int32 accumulators: C[m][n] = sum_k A_q[m][k] * W_q[n][k]. */
+int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, int K,
+                        int32_t* C, void* stream);
+
+/* GEMM + epilogue on pre-quantised activations: for each row m, the
+ * LinearForward result for codes A_q[m] with scale_A[m] and zp_A = 0, then
+ * `activation`.  p->scale_A and p->zp_A are ignored. */
+int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64_t M,
+                                        const int8_t* A_q, const float* scale_A, float* C,
+                                        int activation, void* stream);
+
+/* ---- FP8 E4M3 (cpp/include/neuroflow/fp8_e4m3.h) ---------------------------- */
+
+/* Replaces fp32_array_to_e4m3_bits (fp8_e4m3.h:286-290). */
+int nflow_fp8_e4m3_to_bits(const float* in, uint8_t* out, int64_t n, void* stream);
+
+/* Replaces e4m3_bits_to_fp32_array (fp8_e4m3.h:295-299). */
+int nflow_fp8_e4m3_from_bits(const uint8_t* in, float* out, int64_t n, void* stream);
+
+/* Replaces fp8_e4m3_per_tensor_fake_quant (fp8_e4m3.h:312-334); in == out
+ * is allowed. */
+int nflow_fp8_e4m3_fake_quant(const float* in, float scale, float* out, int64_t n,
+                              void* stream);
+
+/* Per-token FP8: scale_A[m] = absmax(row m)/448 (1.0f for a zero row); codes
+ * are fp32_to_e4m3_bits(clamp(a * (1/scale_A[m]), -448, 448)), the
+ * scale-down of fp8_e4m3.h:319-327. */
+int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q,
+                                 float* scale_A, void* stream);
+
+/* Fused FP8 layer: per-token FP8 quantise -> FP8 MFMA GEMM with fp32
+ * accumulation -> (scale_W[n] * scale_A[m]) * acc + bias[n] -> activation.
+ * No FP8 GEMM exists in the reference; its FP8 path is fake-quant followed by
+ * the FP32 Linear loop (fp8_e4m3.h:312-334, fno.cpp:68-79). */
+int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M,
+                                       const float* A, float* C, float* scale_A_out,
+                                       int activation, void* stream);
+
+/* fp32 accumulators of the FP8 GEMM: C[m][n] = sum_k dec(A_q[m][k]) * dec(W_q[n][k]). */
+int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K,
+                       float* C, void* stream);
+
+/* GEMM + epilogue on pre-quantised FP8 activations with per-row scales. */
+int nflow_fp8_linear_forward_quantised(const nflow_fp8_linear_params* p, int64_t M,
+                                       const uint8_t* A_q, const float* scale_A, float* C,
+                                       int activation, void* stream);
+
+/* ---- one-time weight blob preparation (HOST pointers, CPU) ------------------
+ * Run once per layer when the blobs are built (EnableInt8Gemm, runtime.cpp:
+ * 155-166); the results are then uploaded to device memory by the caller. */
+
+/* Replaces fno::QuantiseWeight2D (cpp/src/fno.cpp:325-358): W_q =
+ * clamp(std::round(W / s_c) + zp_c) computed in float, and
+ * sum_w[c] = sum_i (W_q[c,i] - zp_c).  sum_w may be NULL. */
+int nflow_host_quantise_weight_2d(const float* W, int out_features, int in_features,
+                                  const float* scales, const int32_t* zero_points,
+                                  int8_t* W_q, int32_t* sum_w);
+
+/* Per-channel symmetric scales: absmax(row c) / qmax (1.0f for a zero row);
+ * qmax = 127 for INT8, 448 for FP8 E4M3. */
+int nflow_host_per_channel_scales(const float* W, int out_features, int in_features,
+                                  float qmax, float* scales);
+
+/* Per-channel FP8 E4M3 weights: scales[c] = absmax(row c)/448 (1.0f for a
+ * zero row), W_q = fp32_to_e4m3_bits(clamp(W * (1/scales[c]), -448, 448)). */
+int nflow_host_fp8_quantise_weight(const float* W, int out_features, int in_features,
+                                   uint8_t* W_q, float* scales);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NFLOW_QUANT_H */

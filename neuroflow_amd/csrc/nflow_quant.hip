@@ -1,0 +1,613 @@
+// nflow_quant.hip -- kernels and extern "C" entry points of libnflow_quant
+// (declared in include/nflow_quant.h).
+//
+// Dispatch: the row-tile MFMA kernel (rows_kernel.h) serves every shape with
+// K % 4 == 0, K <= 256 (fp32 input) or K <= 1024 (code input), N % 4 == 0
+// and aligned pointers; anything else goes through the generic path
+// (quantise kernel into a stream-ordered workspace, then one thread per
+// output).  Both paths produce identical bits.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/nflow_quant.h"
+#include "common.h"
+#include "rows_kernel.h"
+#include "status.h"
+
+namespace nfq {
+
+// ---------------------------------------------------------------------------
+// Elementwise / per-row kernels
+// ---------------------------------------------------------------------------
+
+// QuantiseActivation, int8_gemm.cpp:507-520.
+__global__ __launch_bounds__(256) void k_quantise_fixed(const float* __restrict__ A,
+                                                        int8_t* __restrict__ Aq, int64_t n,
+                                                        float s, int32_t zp) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        Aq[i] = static_cast<int8_t>(quant_i8_exact(A[i], s, zp));
+}
+
+// One wave per row: absmax -> scale -> codes (+ sum of codes).
+template <bool FP8>
+__global__ __launch_bounds__(256) void k_quantise_token(const float* __restrict__ A, int64_t M,
+                                                        int K, uint8_t* __restrict__ Aq,
+                                                        float* __restrict__ scale,
+                                                        int32_t* __restrict__ sum_a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); m < M; m += nw) {
+        const float* x = A + m * K;
+        float mx = 0.0f;
+        for (int k = lane; k < K; k += 64) mx = fmaxf(mx, fabsf(x[k]));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float s = (mx == 0.0f) ? 1.0f : mx / (FP8 ? 448.0f : 127.0f);
+        int32_t sa = 0;
+        if constexpr (FP8) {
+            const float inv = (s == 0.0f) ? 1.0f : 1.0f / s;
+            for (int k = lane; k < K; k += 64) Aq[m * K + k] = static_cast<uint8_t>(fp8_quant(x[k], inv));
+        } else {
+            const float inv = 1.0f / s;
+            for (int k = lane; k < K; k += 64) {
+                const int32_t q = quant_i8_token(x[k], s, inv);
+                Aq[m * K + k] = static_cast<uint8_t>(q);
+                sa += q;
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sa += __shfl_xor(sa, o);
+        }
+        if (lane == 0) {
+            scale[m] = s;
+            if (sum_a) sum_a[m] = sa;
+        }
+    }
+}
+
+// PrecomputeSumW, int8_gemm.cpp:479-496: one wave per output row.
+__global__ __launch_bounds__(256) void k_sum_w(const int8_t* __restrict__ W,
+                                               const int32_t* __restrict__ zp, int K, int N,
+                                               int32_t* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= N) return;
+    uint32_t acc = 0;
+    for (int i = lane; i < K; i += 64)
+        acc += static_cast<uint32_t>(static_cast<int32_t>(W[static_cast<int64_t>(o) * K + i]) - zp[o]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s);
+    if (lane == 0) out[o] = static_cast<int32_t>(acc);
+}
+
+__global__ __launch_bounds__(256) void k_e4m3_encode(const float* __restrict__ in,
+                                                     uint8_t* __restrict__ out, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        out[i] = static_cast<uint8_t>(e4m3_encode(in[i]));
+}
+
+__global__ __launch_bounds__(256) void k_e4m3_decode(const uint8_t* __restrict__ in,
+                                                     float* __restrict__ out, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        out[i] = e4m3_decode(in[i]);
+}
+
+// fp8_e4m3_per_tensor_fake_quant, fp8_e4m3.h:312-334 (in == out allowed).
+__global__ __launch_bounds__(256) void k_fp8_fake_quant(const float* in, float scale, float* out,
+                                                        int64_t n) {
+    const float inv = (scale == 0.0f) ? 1.0f : (1.0f / scale);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride)
+        out[i] = e4m3_decode(fp8_quant(in[i], inv)) * scale;
+}
+
+// Generic product + epilogue: one thread per output, any K / N / alignment.
+// Codes are read from Aq (already quantised); per-row scale from scale_in
+// (or the fixed a.scale_A when scale_in is null).
+template <bool FP8, int OUT>
+__global__ __launch_bounds__(256) void k_generic(RowsArgs a, int act) {
+    const int64_t total = a.M * a.N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    const int K = a.K;
+    const int Kd = std::min(K, a.kb_dot * 64);
+    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+         idx += stride) {
+        const int64_t m = idx / a.N;
+        const int n = static_cast<int>(idx - m * a.N);
+        const uint8_t* x = a.Aq + m * K;
+        const uint8_t* w = a.W + static_cast<int64_t>(n) * K;
+        if constexpr (FP8) {
+            float acc = 0.0f;
+            for (int k = 0; k < Kd; ++k) acc += e4m3_decode(x[k]) * e4m3_decode(w[k]);
+            if constexpr (OUT == OUT_RAW) {
+                static_cast<float*>(a.C)[idx] = acc;
+            } else {
+                const float sa = a.scale_in ? a.scale_in[m] : a.scale_A;
+                const float b = a.bias ? a.bias[n] : 0.0f;
+                static_cast<float*>(a.C)[idx] = activate_rt(dequant_bias(a.sW[n], sa, acc, b), act);
+            }
+        } else {
+            uint32_t D = 0, SA = 0, Sf = 0, Sd = 0;
+            for (int k = 0; k < K; ++k) {
+                const int32_t xv = static_cast<int8_t>(x[k]);
+                const int32_t wv = static_cast<int8_t>(w[k]);
+                SA += static_cast<uint32_t>(xv);
+                Sf += static_cast<uint32_t>(wv);
+                if (k < Kd) {
+                    D += static_cast<uint32_t>(xv * wv);
+                    Sd += static_cast<uint32_t>(wv);
+                }
+            }
+            if constexpr (OUT == OUT_RAW) {
+                static_cast<int32_t*>(a.C)[idx] = static_cast<int32_t>(D);
+            } else {
+                const int32_t zpw = a.zpW ? a.zpW[n] : 0;
+                const int32_t swg = a.sumW ? a.sumW[n] : 0;
+                const IntEpi e = int_epi_consts(a.formula, K, a.zp_A, zpw, swg, a.sumW != nullptr,
+                                                static_cast<int32_t>(Sf), static_cast<int32_t>(Sd));
+                const float t = int_epi_value(e, static_cast<int32_t>(D), static_cast<int32_t>(SA));
+                const float sa = a.scale_in ? a.scale_in[m] : a.scale_A;
+                const float b = a.bias ? a.bias[n] : 0.0f;
+                static_cast<float*>(a.C)[idx] = activate_rt(dequant_bias(a.sW[n], sa, t, b), act);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launch helpers
+// ---------------------------------------------------------------------------
+
+static int num_cus() {
+    static int cached = 0;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached == 0) {
+        int dev = 0;
+        int cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            cu > 0)
+            cached = cu;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
+static unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_per_cu) {
+    const int64_t want = (work_items + per_block - 1) / per_block;
+    const int64_t cap = static_cast<int64_t>(num_cus()) * max_blocks_per_cu;
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min(want, cap)));
+}
+
+static hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+static bool aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Row-tile kernel eligibility for the given input mode.
+static bool rows_ok(const RowsArgs& a, int in_mode) {
+    if (a.K % 4 != 0 || a.N % 4 != 0) return false;
+    if (in_mode == IN_CODES) {
+        if (a.K > 1024 || !aligned(a.Aq, 4)) return false;
+    } else {
+        if (a.K > 256 || !aligned(a.A, 16)) return false;
+    }
+    return aligned(a.W, 4) && aligned(a.C, 16);
+}
+
+template <int KB, bool FP8, int IN, int OUT, int ACT>
+static void launch_rows_kb(const RowsArgs& a, hipStream_t st) {
+    const int64_t tiles = (a.M + 15) / 16;
+    const unsigned grid = grid_for(tiles, 4, 8);
+    if (a.N <= 64)
+        hipLaunchKernelGGL((k_rows<KB, FP8, IN, OUT, ACT, true>), dim3(grid), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_rows<KB, FP8, IN, OUT, ACT, false>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <bool FP8, int IN, int OUT, int ACT>
+static void launch_rows_act(const RowsArgs& a, hipStream_t st) {
+    const int kb = (a.K + 63) / 64;
+    if (kb <= 1) launch_rows_kb<1, FP8, IN, OUT, ACT>(a, st);
+    else if (kb <= 2) launch_rows_kb<2, FP8, IN, OUT, ACT>(a, st);
+    else if (kb <= 4) launch_rows_kb<4, FP8, IN, OUT, ACT>(a, st);
+    else if constexpr (IN == IN_CODES) {
+        if (kb <= 8) launch_rows_kb<8, FP8, IN, OUT, ACT>(a, st);
+        else launch_rows_kb<16, FP8, IN, OUT, ACT>(a, st);
+    }
+}
+
+template <bool FP8, int IN, int OUT>
+static void launch_rows(const RowsArgs& a, int act, hipStream_t st) {
+    if constexpr (OUT == OUT_RAW) {
+        launch_rows_act<FP8, IN, OUT, ACT_NONE>(a, st);
+    } else {
+        if (act == ACT_RELU) launch_rows_act<FP8, IN, OUT, ACT_RELU>(a, st);
+        else if (act == ACT_GELU_TANH) launch_rows_act<FP8, IN, OUT, ACT_GELU_TANH>(a, st);
+        else launch_rows_act<FP8, IN, OUT, ACT_NONE>(a, st);
+    }
+}
+
+template <bool FP8, int OUT>
+static void launch_generic(const RowsArgs& a, int act, hipStream_t st) {
+    const unsigned grid = grid_for(a.M * a.N, 256, 16);
+    hipLaunchKernelGGL((k_generic<FP8, OUT>), dim3(grid), dim3(256), 0, st, a, act);
+}
+
+static int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(NFLOW_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
+    return NFLOW_OK;
+}
+
+// Stream-ordered scratch for the generic path (released on the same stream).
+struct Scratch {
+    void* p = nullptr;
+    hipStream_t st = nullptr;
+    hipError_t err = hipSuccess;
+    Scratch(size_t bytes, hipStream_t s) : st(s) { err = hipMallocAsync(&p, std::max<size_t>(bytes, 256), s); }
+    ~Scratch() {
+        if (p) (void)hipFreeAsync(p, st);
+    }
+};
+
+static int kb_dot_for(int formula, int K) {
+    if (formula == F_ROW_VNNI) return K / 64;   // int8_gemm.cpp:366: vec_end = K - K % 64
+    return (K + 63) / 64;
+}
+
+static int formula_row(int K) { return K <= 4096 ? F_ROW_VNNI : F_ROW_SCALAR; }
+
+// Fixed-scale int8 path shared by LinearForward / rows / batched.
+static int int8_fixed_path(const nflow_int8_linear_params* p, int64_t rows, const float* A, float* C,
+                           int formula, hipStream_t st, const char* what) {
+    RowsArgs a{};
+    a.A = A;
+    a.M = rows;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = reinterpret_cast<const uint8_t*>(p->W_int8);
+    a.sW = p->scale_W;
+    a.zpW = p->zp_W;
+    a.bias = p->bias;
+    a.sumW = p->sum_W_per_row;
+    a.scale_A = p->scale_A;
+    a.zp_A = p->zp_A;
+    a.formula = formula;
+    a.kb_dot = kb_dot_for(formula, a.K);
+    a.C = C;
+    if (rows_ok(a, IN_F32_FIXED)) {
+        launch_rows<false, IN_F32_FIXED, OUT_EPI>(a, ACT_NONE, st);
+        return check_launch(what);
+    }
+    Scratch ws(static_cast<size_t>(rows) * a.K, st);
+    if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, std::string(what) + ": workspace allocation failed");
+    const int64_t n = rows * a.K;
+    hipLaunchKernelGGL(k_quantise_fixed, dim3(grid_for(n, 256, 16)), dim3(256), 0, st, A,
+                       static_cast<int8_t*>(ws.p), n, p->scale_A, p->zp_A);
+    a.Aq = static_cast<const uint8_t*>(ws.p);
+    a.scale_in = nullptr;
+    launch_generic<false, OUT_EPI>(a, ACT_NONE, st);
+    return check_launch(what);
+}
+
+static int check_params(const nflow_int8_linear_params* p, const char* what) {
+    if (!p || !p->W_int8 || !p->scale_W || !p->zp_W)
+        return set_error(NFLOW_INVALID_ARG, std::string(what) + ": null input/output");
+    if (p->in_features <= 0 || p->out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, std::string(what) + ": bad feature dims");
+    return NFLOW_OK;
+}
+
+static bool valid_act(int act) { return act == ACT_NONE || act == ACT_RELU || act == ACT_GELU_TANH; }
+
+}  // namespace nfq
+
+using namespace nfq;
+
+extern "C" {
+
+int nflow_quant_abi_version(void) { return NFLOW_QUANT_ABI_VERSION; }
+
+int nflow_int8_quantise_activation(const float* A, int8_t* A_q, int64_t bsz, int in_features,
+                                   float scale_A, int32_t zp_A, void* stream) {
+    clear_error();
+    if (!A || !A_q) return NFLOW_OK;   // the reference returns silently (int8_gemm.cpp:511)
+    const int64_t n = bsz * static_cast<int64_t>(in_features);
+    if (n <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL(k_quantise_fixed, dim3(grid_for(n, 256, 16)), dim3(256), 0,
+                       as_stream(stream), A, A_q, n, scale_A, zp_A);
+    return check_launch("QuantiseActivation");
+}
+
+int nflow_int8_precompute_sum_w(const int8_t* W_int8, const int32_t* zp_W, int in_features,
+                                int out_features, int32_t* sum_W_out, void* stream) {
+    clear_error();
+    if (!W_int8 || !zp_W || !sum_W_out || in_features <= 0 || out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, "PrecomputeSumW: null input or bad dims");
+    hipLaunchKernelGGL(k_sum_w, dim3((out_features + 3) / 4), dim3(256), 0, as_stream(stream),
+                       W_int8, zp_W, in_features, out_features, sum_W_out);
+    return check_launch("PrecomputeSumW");
+}
+
+int nflow_int8_linear_forward(const nflow_int8_linear_params* p, const float* A, float* C,
+                              void* stream) {
+    clear_error();
+    if (!A || !C) return set_error(NFLOW_INVALID_ARG, "Int8Linear: null input/output");
+    int rc = check_params(p, "Int8Linear");
+    if (rc) return rc;
+    return int8_fixed_path(p, 1, A, C, formula_row(p->in_features), as_stream(stream),
+                           "Int8Linear");
+}
+
+int nflow_int8_linear_forward_rows(const nflow_int8_linear_params* p, int64_t rows,
+                                   const float* A, float* C, void* stream) {
+    clear_error();
+    if (!A || !C) return set_error(NFLOW_INVALID_ARG, "Int8Linear: null input/output");
+    int rc = check_params(p, "Int8Linear");
+    if (rc) return rc;
+    if (rows <= 0) return NFLOW_OK;
+    return int8_fixed_path(p, rows, A, C, formula_row(p->in_features), as_stream(stream),
+                           "Int8Linear");
+}
+
+int nflow_int8_linear_forward_batched(const nflow_int8_linear_params* p, int64_t bsz,
+                                      const float* A, float* C, void* stream) {
+    clear_error();
+    if (bsz <= 0) return NFLOW_OK;
+    if (!A || !C) return set_error(NFLOW_INVALID_ARG, "LinearForwardBatched: null A or C");
+    int rc = check_params(p, "LinearForwardBatched");
+    if (rc) return rc;
+    return int8_fixed_path(p, bsz, A, C, F_BATCHED, as_stream(stream), "LinearForwardBatched");
+}
+
+int nflow_int8_quantise_per_token(const float* A, int64_t M, int K, int8_t* A_q, float* scale_A,
+                                  int32_t* sum_a, void* stream) {
+    clear_error();
+    if (!A || !A_q || !scale_A) return set_error(NFLOW_INVALID_ARG, "quantise_per_token: null pointer");
+    if (K <= 0) return set_error(NFLOW_INVALID_ARG, "quantise_per_token: K <= 0");
+    if (M <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL((k_quantise_token<false>), dim3(grid_for(M, 4, 16)), dim3(256), 0,
+                       as_stream(stream), A, M, K, reinterpret_cast<uint8_t*>(A_q), scale_A, sum_a);
+    return check_launch("quantise_per_token");
+}
+
+int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64_t M,
+                                        const float* A, float* C, float* scale_A_out,
+                                        int activation, void* stream) {
+    clear_error();
+    if (!A || !C || !p || !p->W_int8 || !p->scale_W)
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: null input/output");
+    if (p->in_features <= 0 || p->out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: bad feature dims");
+    if (!valid_act(activation))
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: unknown activation");
+    if (M <= 0) return NFLOW_OK;
+    hipStream_t st = as_stream(stream);
+    RowsArgs a{};
+    a.A = A;
+    a.M = M;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = reinterpret_cast<const uint8_t*>(p->W_int8);
+    a.sW = p->scale_W;
+    a.zpW = p->zp_W;
+    a.bias = p->bias;
+    a.sumW = p->sum_W_per_row;
+    a.zp_A = 0;
+    a.formula = formula_row(a.K);
+    a.kb_dot = kb_dot_for(a.formula, a.K);
+    a.C = C;
+    a.scale_out = scale_A_out;
+    if (rows_ok(a, IN_F32_TOKEN)) {
+        launch_rows<false, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
+        return check_launch("linear_forward_per_token");
+    }
+    // Split path: quantise into a workspace, then the product.
+    const size_t codes = static_cast<size_t>(M) * a.K;
+    Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float), st);
+    if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_per_token: workspace allocation failed");
+    uint8_t* q = static_cast<uint8_t*>(ws.p);
+    float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
+    hipLaunchKernelGGL((k_quantise_token<false>), dim3(grid_for(M, 4, 16)), dim3(256), 0, st, A, M,
+                       a.K, q, sc, static_cast<int32_t*>(nullptr));
+    if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
+    a.Aq = q;
+    a.scale_in = sc;
+    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, st);
+    else launch_generic<false, OUT_EPI>(a, activation, st);
+    return check_launch("linear_forward_per_token");
+}
+
+int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, int K, int32_t* C,
+                        void* stream) {
+    clear_error();
+    if (!A_q || !W_q || !C) return set_error(NFLOW_INVALID_ARG, "gemm_i32: null pointer");
+    if (N <= 0 || K <= 0) return set_error(NFLOW_INVALID_ARG, "gemm_i32: bad dims");
+    if (M <= 0) return NFLOW_OK;
+    RowsArgs a{};
+    a.Aq = reinterpret_cast<const uint8_t*>(A_q);
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.W = reinterpret_cast<const uint8_t*>(W_q);
+    a.kb_dot = (K + 63) / 64;
+    a.C = C;
+    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    else launch_generic<false, OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    return check_launch("gemm_i32");
+}
+
+int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64_t M,
+                                        const int8_t* A_q, const float* scale_A, float* C,
+                                        int activation, void* stream) {
+    clear_error();
+    if (!A_q || !scale_A || !C || !p || !p->W_int8 || !p->scale_W)
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_quantised: null input/output");
+    if (p->in_features <= 0 || p->out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_quantised: bad feature dims");
+    if (!valid_act(activation))
+        return set_error(NFLOW_INVALID_ARG, "linear_forward_quantised: unknown activation");
+    if (M <= 0) return NFLOW_OK;
+    RowsArgs a{};
+    a.Aq = reinterpret_cast<const uint8_t*>(A_q);
+    a.scale_in = scale_A;
+    a.M = M;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = reinterpret_cast<const uint8_t*>(p->W_int8);
+    a.sW = p->scale_W;
+    a.zpW = p->zp_W;
+    a.bias = p->bias;
+    a.sumW = p->sum_W_per_row;
+    a.zp_A = 0;
+    a.formula = formula_row(a.K);
+    a.kb_dot = kb_dot_for(a.formula, a.K);
+    a.C = C;
+    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
+    else launch_generic<false, OUT_EPI>(a, activation, as_stream(stream));
+    return check_launch("linear_forward_quantised");
+}
+
+int nflow_fp8_e4m3_to_bits(const float* in, uint8_t* out, int64_t n, void* stream) {
+    clear_error();
+    if (!in || !out) return set_error(NFLOW_INVALID_ARG, "fp8_e4m3_to_bits: null pointer");
+    if (n <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL(k_e4m3_encode, dim3(grid_for(n, 256, 16)), dim3(256), 0, as_stream(stream),
+                       in, out, n);
+    return check_launch("fp8_e4m3_to_bits");
+}
+
+int nflow_fp8_e4m3_from_bits(const uint8_t* in, float* out, int64_t n, void* stream) {
+    clear_error();
+    if (!in || !out) return set_error(NFLOW_INVALID_ARG, "fp8_e4m3_from_bits: null pointer");
+    if (n <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL(k_e4m3_decode, dim3(grid_for(n, 256, 16)), dim3(256), 0, as_stream(stream),
+                       in, out, n);
+    return check_launch("fp8_e4m3_from_bits");
+}
+
+int nflow_fp8_e4m3_fake_quant(const float* in, float scale, float* out, int64_t n, void* stream) {
+    clear_error();
+    if (!in || !out) return set_error(NFLOW_INVALID_ARG, "fp8_e4m3_fake_quant: null pointer");
+    if (n <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL(k_fp8_fake_quant, dim3(grid_for(n, 256, 16)), dim3(256), 0,
+                       as_stream(stream), in, scale, out, n);
+    return check_launch("fp8_e4m3_fake_quant");
+}
+
+int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q, float* scale_A,
+                                 void* stream) {
+    clear_error();
+    if (!A || !A_q || !scale_A) return set_error(NFLOW_INVALID_ARG, "fp8_quantise_per_token: null pointer");
+    if (K <= 0) return set_error(NFLOW_INVALID_ARG, "fp8_quantise_per_token: K <= 0");
+    if (M <= 0) return NFLOW_OK;
+    hipLaunchKernelGGL((k_quantise_token<true>), dim3(grid_for(M, 4, 16)), dim3(256), 0,
+                       as_stream(stream), A, M, K, A_q, scale_A, static_cast<int32_t*>(nullptr));
+    return check_launch("fp8_quantise_per_token");
+}
+
+static int fp8_check(const nflow_fp8_linear_params* p, int act, const char* what) {
+    if (!p || !p->W_e4m3 || !p->scale_W) return set_error(NFLOW_INVALID_ARG, std::string(what) + ": null input/output");
+    if (p->in_features <= 0 || p->out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, std::string(what) + ": bad feature dims");
+    if (!valid_act(act)) return set_error(NFLOW_INVALID_ARG, std::string(what) + ": unknown activation");
+    return NFLOW_OK;
+}
+
+int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A,
+                                       float* C, float* scale_A_out, int activation, void* stream) {
+    clear_error();
+    if (!A || !C) return set_error(NFLOW_INVALID_ARG, "fp8_linear_forward_per_token: null input/output");
+    int rc = fp8_check(p, activation, "fp8_linear_forward_per_token");
+    if (rc) return rc;
+    if (M <= 0) return NFLOW_OK;
+    hipStream_t st = as_stream(stream);
+    RowsArgs a{};
+    a.A = A;
+    a.M = M;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = p->W_e4m3;
+    a.sW = p->scale_W;
+    a.bias = p->bias;
+    a.kb_dot = (a.K + 63) / 64;
+    a.C = C;
+    a.scale_out = scale_A_out;
+    if (rows_ok(a, IN_F32_TOKEN)) {
+        launch_rows<true, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
+        return check_launch("fp8_linear_forward_per_token");
+    }
+    const size_t codes = static_cast<size_t>(M) * a.K;
+    Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float), st);
+    if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "fp8_linear_forward_per_token: workspace allocation failed");
+    uint8_t* q = static_cast<uint8_t*>(ws.p);
+    float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
+    hipLaunchKernelGGL((k_quantise_token<true>), dim3(grid_for(M, 4, 16)), dim3(256), 0, st, A, M,
+                       a.K, q, sc, static_cast<int32_t*>(nullptr));
+    if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
+    a.Aq = q;
+    a.scale_in = sc;
+    if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_EPI>(a, activation, st);
+    else launch_generic<true, OUT_EPI>(a, activation, st);
+    return check_launch("fp8_linear_forward_per_token");
+}
+
+int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K, float* C,
+                       void* stream) {
+    clear_error();
+    if (!A_q || !W_q || !C) return set_error(NFLOW_INVALID_ARG, "fp8_gemm_f32: null pointer");
+    if (N <= 0 || K <= 0) return set_error(NFLOW_INVALID_ARG, "fp8_gemm_f32: bad dims");
+    if (M <= 0) return NFLOW_OK;
+    RowsArgs a{};
+    a.Aq = A_q;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.W = W_q;
+    a.kb_dot = (K + 63) / 64;
+    a.C = C;
+    if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    else launch_generic<true, OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    return check_launch("fp8_gemm_f32");
+}
+
+int nflow_fp8_linear_forward_quantised(const nflow_fp8_linear_params* p, int64_t M,
+                                       const uint8_t* A_q, const float* scale_A, float* C,
+                                       int activation, void* stream) {
+    clear_error();
+    if (!A_q || !scale_A || !C) return set_error(NFLOW_INVALID_ARG, "fp8_linear_forward_quantised: null input/output");
+    int rc = fp8_check(p, activation, "fp8_linear_forward_quantised");
+    if (rc) return rc;
+    if (M <= 0) return NFLOW_OK;
+    RowsArgs a{};
+    a.Aq = A_q;
+    a.scale_in = scale_A;
+    a.M = M;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = p->W_e4m3;
+    a.sW = p->scale_W;
+    a.bias = p->bias;
+    a.kb_dot = (a.K + 63) / 64;
+    a.C = C;
+    if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
+    else launch_generic<true, OUT_EPI>(a, activation, as_stream(stream));
+    return check_launch("fp8_linear_forward_quantised");
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+"""The C-ABI library (no GPU needed): it loads, exports every entry point
+include/nflow_quant.h declares, the ctypes table matches the header, status
+codes equal nflow::StatusCode, and the host-side weight-blob builders match
+the oracle bit for bit."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from neuroflow_amd import _lib
+from neuroflow_amd import quant as Q
+from neuroflow_amd import workloads as WL
+from oracle import oracle as O
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nflow_quant.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(nflow_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_surface():
+    names = declared_functions()
+    assert len(names) >= 20
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_abi_version_and_status_values():
+    assert _lib.lib().nflow_quant_abi_version() == 1
+    text = HEADER.read_text()
+    # nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37
+    for name, val in [("NFLOW_OK", 0), ("NFLOW_INVALID_ARG", 1), ("NFLOW_FILE_NOT_FOUND", 2),
+                      ("NFLOW_PARSE_ERROR", 3), ("NFLOW_SHAPE_MISMATCH", 4),
+                      ("NFLOW_UNSUPPORTED_OP", 5), ("NFLOW_INTERNAL", 99)]:
+        assert re.search(rf"\b{name}\s*=\s*{val}\b", text), name
+
+
+def test_host_weight_quantise_matches_oracle():
+    W = WL.uniform(40, (96, 200), -0.3, 0.3)
+    W[3] = 0.0
+    W[4, 5] = np.nan
+    s = Q.per_channel_scales(W, 127.0)
+    s_ref = O.per_channel_scales(W, 127.0)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    zps = np.round(WL.uniform(41, (96,), -9, 9)).astype(np.int32)
+    q, sw = Q.quantise_weight_2d(W, s_ref, zps)
+    q_ref, sw_ref = O.quantise_weight_2d(W, s_ref, zps)
+    assert np.array_equal(q, q_ref) and np.array_equal(sw, sw_ref)
+
+
+def test_host_fp8_weight_blob_matches_oracle():
+    W = WL.uniform(42, (64, 128), -0.2, 0.2)
+    W[0] = 0.0
+    W[1, :3] = [1e-9, -1e-9, 0.5]
+    q, s = Q.fp8_quantise_weight(W)
+    q_ref, s_ref = O.quantise_weight_fp8(W)
+    assert np.array_equal(q, q_ref) and np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_host_entry_points_reject_bad_arguments():
+    with pytest.raises(_lib.NflowError) as ei:
+        Q.per_channel_scales(np.zeros((0, 4), np.float32), 127.0)
+    assert ei.value.code == _lib.INVALID_ARG
+    assert b"bad dims" in _lib.lib().nflow_last_error()

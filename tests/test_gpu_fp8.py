@@ -1,0 +1,104 @@
+"""GPU parity of the FP8 E4M3 path: codec bytes bit-exact with the oracle
+(fp8_e4m3.h), GEMM outputs within 1e-5 rel / 1e-6 abs."""
+import numpy as np
+import pytest
+import torch
+
+from neuroflow_amd import quant as Q
+from neuroflow_amd import workloads as WL
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def _cu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def test_codec_strided_bit_patterns(gpu):
+    """fp32 bit patterns k * 7 (k < 2^32 / 7: every exponent, sign and
+    mantissa residue) encoded on the device against the oracle."""
+    stride, chunk = 7, 1 << 24
+    total = (1 << 32) // stride
+    for c0 in range(0, total, chunk):
+        n = min(chunk, total - c0)
+        start = c0 * stride
+        bits = torch.arange(start, start + n * stride, stride, dtype=torch.int64, device="cuda")
+        x = (bits - (bits >= 2**31).to(torch.int64) * 2**32).to(torch.int32).view(torch.float32)
+        got = _host(Q.fp8_e4m3_to_bits(x))
+        ref = O.e4m3_encode_bits_stride(start, stride, n)
+        assert np.array_equal(got, ref), hex(start)
+
+
+def test_decode_and_fake_quant(gpu):
+    b = np.arange(256, dtype=np.uint8)
+    d = _host(Q.fp8_e4m3_from_bits(_cu(b)))
+    assert np.array_equal(d.view(np.uint32), O.e4m3_decode(b).view(np.uint32))
+    x = (WL.uniform(30, (100000,)) - 0.5) * 1200.0
+    for scale in (1.0, 2.5, 0.0, 1e-3):
+        got = _host(Q.fp8_e4m3_fake_quant(_cu(x), scale))
+        assert np.array_equal(got.view(np.uint32), O.fp8_fake_quant(x, scale).view(np.uint32))
+    # numpy in -> numpy out, like neuroflow_cpp
+    assert np.array_equal(Q.fp8_e4m3_to_bits(x[:100]), O.e4m3_encode(x[:100]))
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (999, 64), (100, 256), (10, 100)])
+def test_quantise_per_token_fp8(gpu, M, K):
+    x = 2.0 * WL.normal(31, (M, K))
+    x[0, :4] = [1e-4, -1e-5, 448.0, 0.0]
+    q, s = Q.fp8_quantise_per_token(_cu(x))
+    q_ref, s_ref = O.quantise_per_token_fp8(x)
+    assert np.array_equal(_host(s).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(_host(q), q_ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 64, 64), (300, 768, 256), (40, 64, 100)])
+def test_fp8_gemm_accumulators(gpu, M, N, K):
+    x = 2.0 * WL.normal(32, (M, K))
+    W = WL.uniform(33, (N, K), -0.125, 0.125)
+    qa, _ = O.quantise_per_token_fp8(x)
+    qw, _ = O.quantise_weight_fp8(W)
+    got = _host(Q.fp8_gemm_f32(_cu(qa), _cu(qw))).astype(np.float64)
+    exact = O.gemm_fp8_exact(qa, qw)
+    mag = np.abs(O.e4m3_decode(qa)).astype(np.float64) @ np.abs(O.e4m3_decode(qw)).astype(np.float64).T
+    # fp32 accumulation of exact products: |err| <= K * 2^-24 * sum|a_k w_k|
+    assert np.all(np.abs(got - exact) <= K * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 64, 64), (200, 768, 256), (30, 64, 100)])
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_fp8_layer(gpu, M, N, K, act):
+    x = 2.0 * WL.normal(34, (M, K))
+    x = np.where(WL.uniform(35, (M, K)) < 0.01, 20.0 * x, x).astype(np.float32)
+    W = WL.uniform(36, (N, K), -0.125, 0.125)
+    b = WL.uniform(37, (N,), -0.125, 0.125)
+    layer = Q.Fp8Linear(W, b)
+    qw_ref, sw_ref = O.quantise_weight_fp8(W)
+    assert np.array_equal(layer.W_q, qw_ref)
+    assert np.array_equal(layer.scale_W.view(np.uint32), sw_ref.view(np.uint32))
+    out = _host(layer(_cu(x), act))
+    a = {"none": 0, "gelu": 2}[act]
+    qa, sa = O.quantise_per_token_fp8(x)
+    exact = O.layer_fp8_exact(qa, sa, qw_ref, sw_ref, b, a)
+    np.testing.assert_allclose(out, exact, rtol=RTOL, atol=ATOL)
+    # The reference composition (fake-quant, then the fp32 Linear loop of
+    # fno.cpp:68-79 with the bias as the first term) carries its own rounding:
+    # a sequential fp32 sum of K terms is off the exact sum by up to
+    # K * 2^-24 * sum|terms|.  At K = 64 (the FNO2d FP8 shape) that stays
+    # inside 1e-5 / 1e-6; for wider K the bound is added to the tolerance.
+    composed, _, _ = O.layer_fp8_composed(x, W, b, a)
+    if K <= 64:
+        np.testing.assert_allclose(out, composed, rtol=RTOL, atol=ATOL)
+    else:
+        terms = (np.abs(O.e4m3_decode(qa)) * sa[:, None]).astype(np.float64) @ \
+            (np.abs(O.e4m3_decode(qw_ref)) * sw_ref[:, None]).astype(np.float64).T
+        own = K * 2.0 ** -24 * (terms + np.abs(b)[None, :])
+        assert np.all(np.abs(out.astype(np.float64) - composed) <=
+                      ATOL + RTOL * np.abs(composed) + own)

@@ -1,0 +1,164 @@
+"""GPU parity of the INT8 path against the oracle (bit-exact codes, int32
+accumulators and dequantised outputs; GELU within 1e-5 rel / 1e-6 abs)."""
+import numpy as np
+import pytest
+import torch
+
+from neuroflow_amd import quant as Q
+from neuroflow_amd import workloads as WL
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6   # floating-point tolerance for the fp32 outputs
+
+
+def _cu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32),
+                          np.asarray(b, np.float32).view(np.uint32))
+
+
+def _weights(N, K, sid, zp=False):
+    W = WL.uniform(sid, (N, K), -0.125, 0.125)
+    s = O.per_channel_scales(W, 127.0)
+    zps = (WL.uniform(sid + 1, (N,), -6, 6).astype(np.int32) if zp else np.zeros(N, np.int32))
+    q, sw = O.quantise_weight_2d(W, s, zps)
+    b = WL.uniform(sid + 2, (N,), -0.1, 0.1)
+    return W, q, s, zps, sw, b
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (37, 64), (1000, 64), (513, 256), (77, 100), (64, 1024),
+                                 (33, 4)])
+def test_quantise_per_token_codes_bit_exact(gpu, M, K):
+    A = WL.normal(11, (M, K)) * 3.0
+    A[0, 0] = 0.0
+    if M > 2:
+        A[1] = 0.0                      # an all-zero row -> scale 1
+        A[2, : min(K, 8)] = np.array([1.5, -2.5, 0.5, -0.5, 127.0, -127.0, 2.5, 3.5][: min(K, 8)])
+    q, s, sa = Q.quantise_per_token(_cu(A))
+    q_ref, s_ref, sa_ref = O.quantise_per_token_i8(A)
+    assert _bits_equal(_host(s), s_ref)
+    assert np.array_equal(_host(q), q_ref)
+    assert np.array_equal(_host(sa), sa_ref)
+
+
+def test_quantise_per_token_ties_and_specials(gpu):
+    # Rows whose quotients land exactly on k + 0.5 (absmax 127 -> scale 1).
+    K = 64
+    A = np.zeros((4, K), np.float32)
+    A[:, 0] = 127.0
+    A[0, 1:] = np.arange(1, K, dtype=np.float32) * 0.5 - 16.0
+    A[1, 1:] = -(np.arange(1, K, dtype=np.float32) * 0.5)
+    A[2, 1:5] = [np.nan, 3.5, -3.5, 1e-30]
+    A[3, 0] = np.inf
+    A[3, 1:4] = [1.0, -np.inf, 0.0]
+    q, s, _ = Q.quantise_per_token(_cu(A))
+    q_ref, s_ref, _ = O.quantise_per_token_i8(A)
+    assert _bits_equal(_host(s), s_ref)
+    assert np.array_equal(_host(q), q_ref)
+
+
+@pytest.mark.parametrize("scale,zp", [(0.05, 0), (0.05, 3), (0.03, -7), (0.0, 0), (1.0, 100)])
+def test_quantise_activation_bit_exact(gpu, scale, zp):
+    A = WL.normal(12, (300, 96)) * 4.0
+    A[0, :6] = [np.nan, np.inf, -np.inf, 3e9, -3e9, 0.5]
+    got = _host(Q.quantise_activation(_cu(A), scale, zp))
+    assert np.array_equal(got, O.quantise_activation(A, scale, zp))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (100, 64, 64), (1000, 48, 64), (257, 768, 256),
+                                   (33, 256, 1024), (50, 20, 100), (64, 1024, 1024)])
+def test_gemm_i32_bit_exact(gpu, M, N, K):
+    A = WL.uniform(13, (M, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
+    W = WL.uniform(14, (N, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
+    A[0, :] = -128
+    W[0, :] = -128
+    got = _host(Q.gemm_i32(_cu(A), _cu(W)))
+    assert np.array_equal(got, O.gemm_i8_i32(A, W))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (1000, 64, 64), (513, 768, 256), (300, 256, 256),
+                                   (40, 64, 100), (16, 64, 4)])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu"])
+def test_per_token_layer(gpu, M, N, K, act):
+    A = WL.normal(15, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 16)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw))
+    out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
+    ref, sa_ref = O.layer_per_token_i8(A, q, s, zps, b, sw, {"none": 0, "relu": 1, "gelu": 2}[act])
+    out = _host(out)
+    assert _bits_equal(_host(sa), sa_ref)
+    if act == "gelu":
+        np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    else:
+        assert _bits_equal(out, ref)        # dequant + bias (+ relu) is bit-exact
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 64, 64), (100, 768, 256), (30, 64, 100)])
+@pytest.mark.parametrize("zp_a", [0, 5])
+@pytest.mark.parametrize("with_sum", [False, True])
+def test_linear_forward_matches_reference_formulas(gpu, M, N, K, zp_a, with_sum):
+    """LinearForward (per row) and LinearForwardBatched, asymmetric weights."""
+    A = WL.normal(17, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 18, zp=True)
+    sumW = sw if with_sum else None
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), scale_A=0.02, zp_A=zp_a,
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    rc, ref_rows = O.linear_forward_rows(A, q, s, zps, b, 0.02, zp_a, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(A))), ref_rows)
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(A[0]))), ref_rows[0])
+    rc, ref_b = O.linear_forward_batched(A, q, s, zps, b, 0.02, zp_a, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(A))), ref_b)
+
+
+def test_quantised_entry_matches_fused(gpu):
+    M, N, K = 4096, 1024, 1024
+    A = np.maximum(WL.normal(19, (M, K)), 0)
+    W = WL.kaiming_uniform(20, N, K)
+    layer = Q.Int8Linear(W, WL.uniform(21, (N,), -0.03, 0.03))
+    Aq, sa, _ = Q.quantise_per_token(_cu(A))
+    y1 = _host(Q.linear_forward_quantised(layer.params, Aq, sa, "relu"))
+    y2 = _host(layer(_cu(A), "relu"))
+    assert _bits_equal(y1, y2)
+    ref, _ = O.layer_per_token_i8(A[:64], layer.W_q, layer.scale_W, None,
+                                  WL.uniform(21, (N,), -0.03, 0.03), layer.sum_W, 1)
+    assert _bits_equal(y1[:64], ref)
+
+
+def test_precompute_sum_w(gpu):
+    _, q, s, zps, sw, b = _weights(300, 200, 22, zp=True)
+    got = _host(Q.precompute_sum_w(_cu(q), _cu(zps)))
+    assert np.array_equal(got, O.precompute_sum_w(q, zps))
+
+
+def test_status_codes(gpu):
+    from neuroflow_amd._lib import NflowError
+    _, q, s, zps, sw, b = _weights(64, 64, 23)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b))
+    x = torch.zeros(0, 64, device="cuda")
+    assert Q.linear_forward_batched(p, x).shape == (0, 64)        # bsz <= 0 -> Ok, no work
+    with pytest.raises(ValueError):
+        Q.linear_forward_per_token(p, torch.zeros(4, 32, device="cuda"))
+    with pytest.raises(ValueError):
+        Q.linear_forward_per_token(p, torch.zeros(4, 64, device="cuda"), activation="swish")
+    import ctypes
+    from neuroflow_amd import _lib
+    ps = p.c_struct()
+    ps.W_int8 = None
+    rc = _lib.lib().nflow_int8_linear_forward(ctypes.byref(ps), None, None, None)
+    assert rc == _lib.INVALID_ARG
+    assert b"null" in _lib.lib().nflow_last_error()
+    with pytest.raises(NflowError) as ei:
+        _lib.check(rc, "Int8Linear")
+    assert ei.value.code == _lib.INVALID_ARG
