@@ -1,0 +1,270 @@
+"""Benchmark of the MI355X quantised-GEMM path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]
+
+A step is one pass of the hot path over one batch of synthetic input: for the
+default workload (FNO1d INT8 local-linear stack: batch 256 x 1024 grid points,
+width 64, 4 layers, so each layer is M=262144, K=N=64) that is 4 chained fused
+layers h <- GELU((s_w * s_a) * (W_q q(h)) + b), each one launch of the
+per-token quantise -> INT8 MFMA -> dequant + bias + GELU kernel.
+
+Inputs are resident in HBM before timing.  Steps rotate over enough input /
+output buffer sets (> 1 GB in total) that a step's input is not resident in
+the 256 MB last-level cache.  W untimed warm-up steps run first; then exactly
+K steps are timed with events on the launch stream, bracketed by
+torch.cuda.synchronize().  One JSON line is printed.
+
+Roofline: the dominant kernel is the fused layer; its algorithmic bytes per
+launch are 4MK + 4MN + NK*b_w + 8N and its duration is the timed region
+divided by the number of launches.  The CPU baseline is the reference's own
+INT8 kernel (int8_gemm::LinearForward, AVX-512 VNNI build from oracle/_ref)
+called once per row with that row's scale, plus the tanh GELU, on the host's
+cores, over a bounded sample of the same rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "quantised GEMM TOPS & HBM GB/s (% roofline) + FNO layer samples/s, 1 MI355X"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_PEAK_TOPS = {"int8": 5000.0, "fp8": 5000.0}   # dense, TOPS
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch"])
+    ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--check", action="store_true", default=True)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also time a plain device copy of the layer's bytes (read M*K*4, "
+                         "write M*N*4): the achievable-bandwidth reference and the kernel "
+                         "whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
+    return ap.parse_args()
+
+
+def build_layers(wl, dev):
+    from neuroflow_amd import quant as Q
+    layers = []
+    for L in wl.layers:
+        obj = (Q.Fp8Linear if L.fmt == "fp8" else Q.Int8Linear)(L.W, L.bias, device=dev)
+        layers.append((obj, obj.launcher(L.act), L))
+    return layers
+
+
+def cpu_baseline(wl, layers, args):
+    """Reference kernel on the host cores over a bounded sample of rows."""
+    import numpy as np
+    from oracle import oracle as O
+
+    L0 = wl.layers[0]
+    obj = layers[0][0]
+    cores = O.usable_cores()
+    M_all = wl.M
+    total_rows = M_all * len(wl.layers)          # rows of one step
+    variant = O.ref_variant()
+    if L0.fmt == "int8" and variant is not None and O.ref_available(variant):
+        gelu = L0.act == "gelu"
+        n1 = min(M_all, 16384)
+        t1, _ = O.ref_time_per_token_layer(wl.x[:n1], obj.W_q, obj.scale_W, L0.bias, obj.sum_W,
+                                           threads=1, reps=3, act_gelu=gelu, variant=variant)
+        nN = min(M_all, 262144)
+        tN, _ = O.ref_time_per_token_layer(wl.x[:nN], obj.W_q, obj.scale_W, L0.bias, obj.sum_W,
+                                           threads=cores, reps=3, act_gelu=gelu, variant=variant)
+        rows_s_1, rows_s_N = n1 / t1, nN / tN
+        kind = "reference"
+        sample = (f"int8_gemm::LinearForward ({variant.upper()} build of the reference "
+                  f"sources) once per row with scale_A = absmax/127 + tanh GELU, layer 0 "
+                  f"(K={L0.W.shape[1]}, N={L0.W.shape[0]}): {nN} rows x 3 reps on {cores} "
+                  f"threads, {n1} rows x 3 reps on 1 thread; host {O.host_cpu_model()}")
+    else:
+        # FP8 (no reference kernel exists): the reference's fake-quant + FP32
+        # Linear composition, restated in the oracle, on one thread.
+        n1 = min(M_all, 4096)
+        t0 = time.perf_counter()
+        O.layer_fp8_composed(wl.x[:n1], L0.W, L0.bias, O.ACT_GELU_TANH)
+        t1 = time.perf_counter() - t0
+        rows_s_1 = rows_s_N = n1 / t1
+        cores = 1
+        kind = "port"
+        sample = (f"FP8 E4M3 fake-quant (fp8_e4m3.h:312-334) + FP32 Linear loop (fno.cpp:68-79), "
+                  f"restated in oracle/, {n1} rows of layer 0 on 1 thread (the reference has "
+                  f"no FP8 GEMM); host {O.host_cpu_model()}")
+    to_unit = wl.samples / total_rows          # samples per row-layer
+    return {
+        "value": rows_s_N * to_unit,
+        "unit": "samples/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": sample,
+        "value_1core": rows_s_1 * to_unit,
+        "layer_rows_per_s": rows_s_N,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
+              "(the path shards along rows with no collective; see the design notes)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from neuroflow_amd import workloads as WL
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    wl = WL.WORKLOADS[args.workload]()
+    layers = build_layers(wl, dev)
+    M = wl.M
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+
+    # Buffer sets: input x and one output per layer, rotated across steps.
+    widths = [wl.x.shape[1]] + [L.W.shape[0] for L in wl.layers]
+    set_bytes = sum(4 * M * w for w in widths)
+    n_sets = args.sets or max(2, min(8, -(-1_100_000_000 // set_bytes)))
+    x0 = torch.from_numpy(wl.x).to(dev)
+    sets = []
+    for _ in range(n_sets):
+        bufs = [x0.clone()] + [torch.empty(M, w, dtype=torch.float32, device=dev) for w in widths[1:]]
+        sets.append(bufs)
+    torch.cuda.synchronize()
+
+    def step(i):
+        bufs = sets[i % n_sets]
+        for l, (_, run, L) in enumerate(layers):
+            src = bufs[l] if wl.chained else bufs[0]
+            run(src.data_ptr(), bufs[l + 1].data_ptr(), M, sptr)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    ms_per_step = ms / args.steps
+    launches = args.steps * len(layers)
+    kernel_us = ms * 1e3 / launches
+
+    # Dominant kernel: the most common layer shape (all layers share one shape
+    # in c1-c3; for c4/c5 the bytes/ops are averaged over the step's launches).
+    bytes_step = sum(wl.bytes_per_layer(l) for l in range(len(layers)))
+    ops_step = sum(wl.ops_per_layer(l) for l in range(len(layers)))
+    gbs = bytes_step / (ms_per_step * 1e-3) / 1e9
+    tops = ops_step / (ms_per_step * 1e-3) / 1e12
+    fmt = wl.layers[0].fmt
+    ai = ops_step / bytes_step
+    bound = "hbm" if ai < MFMA_PEAK_TOPS[fmt] * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+    if args.workload.startswith("c5"):
+        bound = "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_PEAK_TOPS[fmt],
+                "unit": "TFLOP/s" if fmt == "fp8" else "TOPS",
+                "frac": round(tops / MFMA_PEAK_TOPS[fmt], 4), "traffic": None}
+    roof.update({"kernel": "nfq::k_rows" if wl.layers[0].W.shape[1] <= 256 else "nfq::k_rows (codes)",
+                 "kernel_avg_us": round(kernel_us, 3),
+                 "bytes_per_launch": bytes_step // len(layers),
+                 "ops_per_launch": ops_step // len(layers),
+                 "tops": round(tops, 2), "gbs": round(gbs, 1)})
+
+    parity = None
+    if args.check:
+        from oracle import oracle as O
+        # Re-run layer 0 on the first rows and compare with the oracle.
+        n = min(M, 512)
+        L0 = wl.layers[0]
+        obj = layers[0][0]
+        y = obj(torch.from_numpy(wl.x[:n]).to(dev), L0.act).cpu().numpy()
+        act = {"none": 0, "relu": 1, "gelu": 2}[L0.act]
+        if L0.fmt == "int8":
+            ref, _ = O.layer_per_token_i8(wl.x[:n], obj.W_q, obj.scale_W, None, L0.bias, obj.sum_W, act)
+        else:
+            qa, sa = O.quantise_per_token_fp8(wl.x[:n])
+            ref = O.layer_fp8_exact(qa, sa, obj.W_q, obj.scale_W, L0.bias, act)
+        parity = bool(np.allclose(y, ref, rtol=1e-5, atol=1e-6))
+
+    copy = None
+    if args.copy_calib:
+        L0 = wl.layers[0]
+        n_in, n_out = M * L0.W.shape[1], M * L0.W.shape[0]
+        srcs = [s_[0] for s_ in sets]
+        dsts = [s_[1] for s_ in sets]
+        for i in range(3):
+            dsts[i % n_sets].view(-1)[:n_out].copy_(srcs[i % n_sets].view(-1)[:n_out])
+        torch.cuda.synchronize()
+        reps = max(20, args.steps)
+        ev0.record(stream)
+        for i in range(reps):
+            dsts[i % n_sets].view(-1)[:n_out].copy_(srcs[i % n_sets].view(-1)[:n_out])
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / reps
+        cbytes = 8 * n_out
+        copy = {"kernel": "torch copy_ (float32)", "bytes_per_launch": cbytes,
+                "avg_us": round(us, 3), "gbs": round(cbytes / (us * 1e-6) / 1e9, 1),
+                "frac_of_peak": round(cbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(wl, layers, args)
+        except Exception as e:  # reported, not fatal: the GPU figure stands alone
+            cpu = {"error": f"{type(e).__name__}: {e}"}
+
+    value = wl.samples / (ms_per_step * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": fmt,
+        "data": "synthetic (seeded SplitMix64 inputs, seeded Kaiming-uniform weights)",
+        "config": {
+            "workload": wl.name,
+            "rows": M,
+            "layers": [list(L.W.shape[::-1]) for L in wl.layers],
+            "samples_per_step": wl.samples,
+            "buffer_sets": n_sets,
+            "parallelism": "single GPU",
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
+    }
+    if copy is not None:
+        out["copy_calibration"] = copy
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -9,7 +9,11 @@ from __future__ import annotations
 import ctypes as C
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libnflow_quant.so"
+import os
+
+# The in-tree build; NFLOW_QUANT_LIB may name another build of the same sources.
+LIB_PATH = Path(os.environ.get("NFLOW_QUANT_LIB") or
+               Path(__file__).resolve().parent / "lib" / "libnflow_quant.so")
 
 # nflow::StatusCode (cpp/include/neuroflow/tensor.h:29-37).
 OK, INVALID_ARG, FILE_NOT_FOUND, PARSE_ERROR, SHAPE_MISMATCH, UNSUPPORTED_OP, INTERNAL = (

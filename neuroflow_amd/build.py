@@ -24,7 +24,7 @@ LIB = LIB_DIR / "libnflow_quant.so"
 ARCH = os.environ.get("NFLOW_OFFLOAD_ARCH", "gfx950")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
-          "-I", str(PKG.parent / "include")]
+          "-I", str(PKG.parent / "include")] + os.environ.get("NFLOW_EXTRA_FLAGS", "").split()
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
@@ -45,26 +45,27 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, lib: Path = LIB) -> Path:
     srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
-    obj_dir = PKG / "_build"
-    obj_dir.mkdir(exist_ok=True)
+    obj_dir = PKG / "_build" / lib.stem
+    obj_dir.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
     objs = [obj_dir / (s.name + ".o") for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         list(ex.map(lambda so: _compile(*so), zip(srcs, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
+    lib.parent.mkdir(parents=True, exist_ok=True)
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
-    build()
+    build(lib=Path(sys.argv[1]).resolve() if len(sys.argv) > 1 else LIB)
     sys.exit(0)

@@ -49,28 +49,34 @@ __device__ __forceinline__ int32_t quant_i8_exact(float a, float s, int32_t zp) 
 // per-token scale) differs from the correctly rounded quotient q = fl(a / s)
 // by at most 1.5 * 2^-23 |t|.  Rounding half away from zero and rounding
 // half to even differ only at k + 0.5, so whenever the distance of |t| from
-// the nearest half-integer, |fract(|t|) - 0.5|, exceeds |t| * 2^-20 (and
-// |t| < 4096, so the conversion is exact), rint(t) == round(q).  Otherwise --
-// about one element in 10^4 -- the exact division and the x86 conversion
-// are used.  NaN / Inf / zero-scale cases all fail `|t| < 4096` and take the
-// exact branch.
-__device__ __forceinline__ int32_t quant_i8_token(float a, float s, float inv_s) {
+// the nearest half-integer, |fract(|t|) - 0.5|, exceeds |t| * 2^-20,
+// rint(t) == round(q) (and |t| < 2^31, so the conversion is exact).
+// quant_i8_fast returns false when that test fails -- about one element in
+// 10^4, and every NaN / Inf / overflowing quotient -- and the caller then
+// uses quant_i8_exact(a, s, 0) for that element.
+__device__ __forceinline__ bool quant_i8_fast(float a, float inv_s, int32_t& q) {
     const float t = a * inv_s;
     const float at = fabsf(t);
     const float dist = fabsf(__builtin_amdgcn_fractf(at) - 0.5f);
-    int32_t q;
-    if (__builtin_expect(at < 4096.0f && dist > __builtin_fmaf(at, 0x1p-20f, 0x1p-40f), 1)) {
-        q = static_cast<int32_t>(rintf(t));
-    } else {
-        q = cvt_i32_x86(roundf(a / s));
-    }
-    return clamp_i8(q);
+    q = clamp_i8(static_cast<int32_t>(rintf(t)));
+    return dist > __builtin_fmaf(at, 0x1p-20f, 0x1p-40f);
 }
 
-// Pack four int8 codes (low byte first) into one dword.
+// Scalar form: per-token code of one element.
+__device__ __forceinline__ int32_t quant_i8_token(float a, float s, float inv_s) {
+    int32_t q;
+    if (!quant_i8_fast(a, inv_s, q)) q = quant_i8_exact(a, s, 0);
+    return q;
+}
+
+// Pack four int8 codes (low byte first) into one dword: two v_perm_b32
+// select the low bytes (selector 0x0c zeroes a byte).
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {
-    return (static_cast<uint32_t>(a) & 0xFFu) | ((static_cast<uint32_t>(b) & 0xFFu) << 8) |
-           ((static_cast<uint32_t>(c) & 0xFFu) << 16) | (static_cast<uint32_t>(d) << 24);
+    const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(b), static_cast<uint32_t>(a),
+                                              0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(d), static_cast<uint32_t>(c),
+                                              0x04000c0cu);
+    return lo | hi;
 }
 
 // Sum of the four signed bytes of a dword (v_dot4_i32_i8 against ones).

@@ -209,14 +209,41 @@ static bool rows_ok(const RowsArgs& a, int in_mode) {
     return aligned(a.W, 4) && aligned(a.C, 16);
 }
 
+// Resident blocks per CU of a kernel (cached per instantiation).
+template <typename Kernel>
+static int resident_blocks(Kernel k) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, 0) != hipSuccess || n < 1) n = 1;
+    return n;
+}
+
+// Persistent launch: one wave per resident slot, each looping over row tiles.
+template <int KB, bool FP8, int IN, int OUT, int ACT, bool HOIST, bool KFULL>
+static void launch_rows_k(const RowsArgs& a, hipStream_t st) {
+    auto kern = k_rows<KB, FP8, IN, OUT, ACT, HOIST, KFULL>;
+    static const int per_cu = resident_blocks(kern);
+    const int64_t tiles = (a.M + 15) / 16;
+    const unsigned grid = grid_for(tiles, 4, per_cu);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
+}
+
+template <int KB, bool FP8, int IN, int OUT, int ACT, bool KFULL>
+static void launch_rows_h(const RowsArgs& a, hipStream_t st) {
+    if constexpr (rows_hoist_fits(KB, FP8)) {
+        if (a.N <= 64) {
+            launch_rows_k<KB, FP8, IN, OUT, ACT, true, KFULL>(a, st);
+            return;
+        }
+    }
+    launch_rows_k<KB, FP8, IN, OUT, ACT, false, KFULL>(a, st);
+}
+
 template <int KB, bool FP8, int IN, int OUT, int ACT>
 static void launch_rows_kb(const RowsArgs& a, hipStream_t st) {
-    const int64_t tiles = (a.M + 15) / 16;
-    const unsigned grid = grid_for(tiles, 4, 8);
-    if (a.N <= 64)
-        hipLaunchKernelGGL((k_rows<KB, FP8, IN, OUT, ACT, true>), dim3(grid), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL((k_rows<KB, FP8, IN, OUT, ACT, false>), dim3(grid), dim3(256), 0, st, a);
+    // The fixed-scale paths (LinearForward / LinearForwardBatched) are not
+    // the hot loop: one instantiation with range checks serves every K.
+    if (IN != IN_F32_FIXED && a.K == KB * 64) launch_rows_h<KB, FP8, IN, OUT, ACT, true>(a, st);
+    else launch_rows_h<KB, FP8, IN, OUT, ACT, false>(a, st);
 }
 
 template <bool FP8, int IN, int OUT, int ACT>

@@ -63,15 +63,24 @@ struct Op {
 };
 
 // Raw code dwords of the weight tile for column tile n0 and K block kb.
+// Branch-free: the column is clamped into range and the value replaced by 0
+// outside it; with KFULL (K a multiple of 64) every k is in range.
+template <bool KFULL>
 __device__ __forceinline__ void load_w_bytes(const uint8_t* __restrict__ W, int K, int N, int n0,
                                              int kb, int r, int g, uint32_t (&w)[4]) {
     const int n = n0 + r;
+    const uint8_t* rowp = W + static_cast<int64_t>(n < N ? n : N - 1) * K;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int k = kb * 64 + j * 16 + g * 4;
-        w[j] = (n < N && k < K)
-                   ? *reinterpret_cast<const uint32_t*>(W + static_cast<int64_t>(n) * K + k)
-                   : 0u;
+        uint32_t v;
+        if constexpr (KFULL) {
+            v = *reinterpret_cast<const uint32_t*>(rowp + k);
+        } else {
+            v = *reinterpret_cast<const uint32_t*>(rowp + (k < K ? k : K - 4));
+            v = k < K ? v : 0u;
+        }
+        w[j] = n < N ? v : 0u;
     }
 }
 
@@ -86,12 +95,12 @@ __device__ __forceinline__ void bytes_to_bf16_op(const uint32_t (&b)[4], uint32_
 
 // Weight operand (in MFMA form) and the partial byte sums used by the INT8
 // epilogue constants.
-template <bool FP8>
+template <bool FP8, bool KFULL>
 __device__ __forceinline__ void load_w_op(const uint8_t* __restrict__ W, int K, int N, int n0,
                                           int kb, int r, int g, uint32_t (&w)[Op<FP8>::DW],
                                           int32_t& psum) {
     uint32_t b[4];
-    load_w_bytes(W, K, N, n0, kb, r, g, b);
+    load_w_bytes<KFULL>(W, K, N, n0, kb, r, g, b);
     if constexpr (FP8) {
         bytes_to_bf16_op(b, w);
         psum = 0;
@@ -134,170 +143,260 @@ __device__ __forceinline__ void mfma_block(const uint32_t (&w)[Op<FP8>::DW],
 
 // Per-lane epilogue constants of one column tile: the lane's four columns
 // n = n0 + 4g + v.  `trivial` (wave-uniform) is set when every INT8 formula
-// constant of the tile is zero, i.e. the result is (float)D.
+// constant of the tile is zero, i.e. the result is (float)D; the constants
+// themselves (needed only otherwise) are kept per lane in `e`, or -- for the
+// hoisted tiles -- in LDS.
 struct ColConsts {
-    float sw[4];
-    float b[4];
-    IntEpi e[4];
+    v4f sw;
+    v4f b;
     bool trivial;
 };
 
-// Sum of the int8 bytes of a weight operand, reduced over the 4 lanes of a
-// row (lane groups g), then gathered so that lane (r, g) holds the value of
-// column n0 + 4g + v in out[v].
-__device__ __forceinline__ void gather_col_sums(int32_t part, int g, int32_t (&out)[4]) {
+// Reduce a lane's partial byte sum over the 4 lanes of a row (lane groups g):
+// every lane (r, g) then holds the sum of column n0 + r.
+__device__ __forceinline__ int32_t row_sum4(int32_t part) {
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) out[v] = __shfl(part, 4 * g + v);
+    return part;
 }
 
+// Column setup for the 16-column tile n0.  Lane (r, g) computes the INT8
+// epilogue constants of column n0 + r from the reduced weight sums (no
+// gathers needed for the triviality test), and loads scale / bias of its own
+// output columns n0 + 4g + v.  The constants of column n0 + r are returned in
+// `mine`; callers that need them per output column gather or stage them.
 template <bool FP8, int OUT>
-__device__ __forceinline__ void col_consts(const RowsArgs& a, int n0, int g, int32_t part_full,
-                                           int32_t part_dot, ColConsts& cc) {
-    int32_t sfull[4], sdot[4];
-    if constexpr (!FP8 && OUT == OUT_EPI) {
-        gather_col_sums(part_full, g, sfull);
-        gather_col_sums(part_dot, g, sdot);
-    }
+__device__ __forceinline__ void col_setup(const RowsArgs& a, int n0, int r, int g,
+                                          int32_t part_full, int32_t part_dot, ColConsts& cc,
+                                          IntEpi& mine, bool load_sw_b) {
     bool nonzero = false;
+    mine = IntEpi{0, 0, 0};
+    if constexpr (!FP8 && OUT == OUT_EPI) {
+        const int32_t sfull = row_sum4(part_full);
+        const int32_t sdot = row_sum4(part_dot);
+        const int c = n0 + r;
+        if (c < a.N) {
+            const int32_t zpw = a.zpW ? a.zpW[c] : 0;
+            const int32_t swg = a.sumW ? a.sumW[c] : 0;
+            mine = int_epi_consts(a.formula, a.K, a.zp_A, zpw, swg, a.sumW != nullptr, sfull, sdot);
+            nonzero = (mine.c0 != 0) | (mine.c1 != 0) | (mine.c2 != 0);
+        }
+    }
+    if (OUT == OUT_EPI && load_sw_b) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int n = n0 + 4 * g + v;
-        const bool ok = n < a.N;
-        cc.sw[v] = ok ? a.sW[n] : 0.0f;
-        cc.b[v] = (ok && a.bias) ? a.bias[n] : 0.0f;
-        if constexpr (!FP8 && OUT == OUT_EPI) {
-            const int32_t zpw = (ok && a.zpW) ? a.zpW[n] : 0;
-            const int32_t swg = (ok && a.sumW) ? a.sumW[n] : 0;
-            cc.e[v] = int_epi_consts(a.formula, a.K, a.zp_A, zpw, swg, a.sumW != nullptr,
-                                     sfull[v], sdot[v]);
-            nonzero |= (cc.e[v].c0 != 0) | (cc.e[v].c1 != 0) | (cc.e[v].c2 != 0);
-        } else {
-            cc.e[v] = IntEpi{0, 0, 0};
+        for (int v = 0; v < 4; ++v) {
+            const int n = n0 + 4 * g + v;
+            const bool ok = n < a.N;
+            cc.sw[v] = ok ? a.sW[n] : 0.0f;
+            cc.b[v] = (ok && a.bias) ? a.bias[n] : 0.0f;
         }
     }
     cc.trivial = !__any(nonzero);
 }
 
+// Gather the constants of the lane's output columns n0 + 4g + v from the
+// lanes that computed them (lane 4g + v holds column n0 + 4g + v).
+__device__ __forceinline__ void gather_consts(const IntEpi& mine, int g, IntEpi (&e)[4]) {
+    const int32_t c2lo = static_cast<int32_t>(static_cast<uint64_t>(mine.c2));
+    const int32_t c2hi = static_cast<int32_t>(static_cast<uint64_t>(mine.c2) >> 32);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int src = 4 * g + v;
+        e[v].c0 = __shfl(mine.c0, src);
+        e[v].c1 = __shfl(mine.c1, src);
+        const uint32_t lo = static_cast<uint32_t>(__shfl(c2lo, src));
+        const uint32_t hi = static_cast<uint32_t>(__shfl(c2hi, src));
+        e[v].c2 = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+    }
+}
+
 template <bool FP8, int ACT, int OUT>
 __device__ __forceinline__ void store_tile(const RowsArgs& a, int64_t row, int n0, int g,
-                                           const v4i& acc_i, const v4f& acc_f,
-                                           const ColConsts& cc, float srow, int32_t SA) {
+                                           const v4i& acc_i, const v4f& acc_f, v4f sw, v4f bias,
+                                           bool trivial, const IntEpi* e, float srow,
+                                           int32_t SA) {
+    // N % 4 == 0 (a dispatch precondition), so a column group is either
+    // entirely inside or entirely outside [0, N).
     if (row >= a.M) return;
     const int nb = n0 + 4 * g;
     if constexpr (OUT == OUT_RAW) {
         if constexpr (FP8) {
-            float* dst = static_cast<float*>(a.C) + row * a.N + nb;
-            if (nb + 3 < a.N) {
-                __builtin_nontemporal_store(acc_f, reinterpret_cast<v4f*>(dst));
-            } else {
-                for (int v = 0; v < 4; ++v)
-                    if (nb + v < a.N) dst[v] = acc_f[v];
-            }
+            if (nb < a.N)
+                __builtin_nontemporal_store(acc_f, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
         } else {
-            int32_t* dst = static_cast<int32_t*>(a.C) + row * a.N + nb;
-            if (nb + 3 < a.N) {
-                __builtin_nontemporal_store(acc_i, reinterpret_cast<v4i*>(dst));
-            } else {
-                for (int v = 0; v < 4; ++v)
-                    if (nb + v < a.N) dst[v] = acc_i[v];
-            }
+            if (nb < a.N)
+                __builtin_nontemporal_store(acc_i, reinterpret_cast<v4i*>(static_cast<int32_t*>(a.C) + row * a.N + nb));
         }
     } else {
         v4f t;
         if constexpr (FP8) {
             t = acc_f;
-        } else if (cc.trivial) {
+        } else if (trivial) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) t[v] = static_cast<float>(acc_i[v]);
         } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) t[v] = int_epi_value(cc.e[v], acc_i[v], SA);
+            for (int v = 0; v < 4; ++v) t[v] = int_epi_value(e[v], acc_i[v], SA);
         }
         v4f y;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) y[v] = activate<ACT>(dequant_bias(cc.sw[v], srow, t[v], cc.b[v]));
-        float* dst = static_cast<float*>(a.C) + row * a.N + nb;
-        if (nb + 3 < a.N) {
-            __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(dst));
-        } else {
-            for (int v = 0; v < 4; ++v)
-                if (nb + v < a.N) dst[v] = y[v];
-        }
+        for (int v = 0; v < 4; ++v) y[v] = activate<ACT>(dequant_bias(sw[v], srow, t[v], bias[v]));
+        if (nb < a.N)
+            __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
     }
 }
 
+// Exact per-token codes of four elements (the rare slow path of the
+// reciprocal quantiser); kept out of line so that the unrolled hot loop does
+// not carry its registers.
+__device__ __attribute__((noinline)) uint32_t pack4_token_exact(v4f v, float s, float inv) {
+    return pack4(quant_i8_token(v[0], s, inv), quant_i8_token(v[1], s, inv),
+                 quant_i8_token(v[2], s, inv), quant_i8_token(v[3], s, inv));
+}
+
+// Activation operand of one row tile, loaded (fp32 input: raw floats; code
+// input: raw code dwords) ahead of its use so the next tile's HBM reads are
+// in flight while the current tile is computed.
+template <int KB, int IN>
+struct TileIn {
+    v4f x[IN == IN_CODES ? 1 : KB][4];
+    uint32_t c[IN == IN_CODES ? KB : 1][4];
+};
+
+template <int KB, int IN, bool KFULL>
+__device__ __forceinline__ void load_tile(const RowsArgs& a, int64_t tile, int r, int g,
+                                          TileIn<KB, IN>& t) {
+    // Rows past M (only in the last tile) re-read row M-1; they are never
+    // stored.  Without KFULL, k past K reads a clamped address and becomes 0.
+    const int K = a.K;
+    const int64_t row = tile * 16 + r;
+    const int64_t rowc = row < a.M ? row : a.M - 1;
+    if constexpr (IN == IN_CODES) {
+        const uint8_t* base = a.Aq + rowc * K;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = kb * 64 + j * 16 + g * 4;
+                if constexpr (KFULL) {
+                    t.c[kb][j] = *reinterpret_cast<const uint32_t*>(base + k);
+                } else {
+                    const uint32_t v = *reinterpret_cast<const uint32_t*>(base + (k < K ? k : K - 4));
+                    t.c[kb][j] = k < K ? v : 0u;
+                }
+            }
+    } else {
+        const float* base = a.A + rowc * K;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = kb * 64 + j * 16 + g * 4;
+                if constexpr (KFULL) {
+                    t.x[kb][j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + k));
+                } else {
+                    const v4f v = __builtin_nontemporal_load(
+                        reinterpret_cast<const v4f*>(base + (k < K ? k : K - 4)));
+                    t.x[kb][j] = k < K ? v : v4f{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+    }
+}
+
+// Waves per SIMD the register budget is sized for (512 / waves VGPRs).
+#ifndef NFQ_ROWS_WAVES_KB1
+#define NFQ_ROWS_WAVES_KB1 3
+#endif
+constexpr int rows_min_waves(int KB, bool FP8) {
+    return KB == 1 ? NFQ_ROWS_WAVES_KB1 : (KB == 2 && !FP8 ? 3 : 2);
+}
+
+// Whether the weight operands of one 64-column chunk fit in registers.
+#ifndef NFQ_ROWS_HOIST_DW
+#define NFQ_ROWS_HOIST_DW 8
+#endif
+constexpr bool rows_hoist_fits(int KB, bool FP8) { return KB * (FP8 ? 8 : 4) <= NFQ_ROWS_HOIST_DW; }
+
 // KB: number of 64-wide K blocks held per lane (K <= 64 * KB).
 // HOIST: N <= 64, so the weight operands and column constants of the single
-// 64-column chunk stay in registers for the whole kernel.
-template <int KB, bool FP8, int IN, int OUT, int ACT, bool HOIST>
-__global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
+// 64-column chunk stay resident (registers; INT8 formula constants in LDS)
+// for the whole kernel.
+template <int KB, bool FP8, int IN, int OUT, int ACT, bool HOIST, bool KFULL>
+__global__ __launch_bounds__(256, rows_min_waves(KB, FP8)) void k_rows(RowsArgs a) {
     constexpr int DW = Op<FP8>::DW;
+    constexpr bool INT_EPI = !FP8 && OUT == OUT_EPI;
     const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
     const int r = lane & 15;
     const int g = lane >> 4;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
     const int64_t ntiles = (a.M + 15) >> 4;
     const int K = a.K;
     const int N = a.N;
     const int kb_dot = a.kb_dot;
 
+    // The first tile's HBM reads go out before the weight setup.
+    int64_t tile = wave;
+    TileIn<KB, IN> nxt;
+    if (tile < ntiles) load_tile<KB, IN, KFULL>(a, tile, r, g, nxt);
+
     // Hoisted weights: operands for the 4 column tiles of columns 0..63.
     uint32_t wh[HOIST ? 4 : 1][HOIST ? KB : 1][DW];
-    ColConsts cch[HOIST ? 4 : 1];
+    bool triv[HOIST ? 4 : 1];
+    __shared__ IntEpi lds_e[HOIST && INT_EPI ? 64 : 1];
+    __shared__ v4f lds_sw[HOIST ? 16 : 1];
+    __shared__ v4f lds_b[HOIST ? 16 : 1];
     if constexpr (HOIST) {
+        // Scale and bias exist only for the dequantising epilogue (the raw
+        // product entry points pass no scale_W).
+        if (OUT == OUT_EPI && threadIdx.x < 64) {
+            const int n = threadIdx.x;
+            reinterpret_cast<float*>(lds_sw)[n] = n < N ? a.sW[n] : 0.0f;
+            reinterpret_cast<float*>(lds_b)[n] = (n < N && a.bias) ? a.bias[n] : 0.0f;
+        }
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             int32_t pf = 0, pd = 0;
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
                 int32_t ps;
-                load_w_op<FP8>(a.W, K, N, nt * 16, kb, r, g, wh[nt][kb], ps);
+                load_w_op<FP8, KFULL>(a.W, K, N, nt * 16, kb, r, g, wh[nt][kb], ps);
                 pf += ps;
                 if (kb < kb_dot) pd += ps;
             }
-            col_consts<FP8, OUT>(a, nt * 16, g, pf, pd, cch[nt]);
+            IntEpi mine;
+            ColConsts cc;
+            col_setup<FP8, OUT>(a, nt * 16, r, g, pf, pd, cc, mine, false);
+            triv[nt] = cc.trivial;
+            if constexpr (INT_EPI) {
+                if (wid == 0 && g == 0) lds_e[nt * 16 + r] = mine;
+            }
         }
+        __syncthreads();
     }
 
-    for (int64_t tile = wave; tile < ntiles; tile += nwaves) {
+    for (; tile < ntiles; tile += nwaves) {
         const int64_t row = tile * 16 + r;
         const bool row_ok = row < a.M;
+        TileIn<KB, IN> cur = nxt;
+        if (tile + nwaves < ntiles) load_tile<KB, IN, KFULL>(a, tile + nwaves, r, g, nxt);
+
         uint32_t xc[KB][DW];
         float srow = 1.0f;
 
         if constexpr (IN == IN_CODES) {
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                uint32_t b[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k = kb * 64 + j * 16 + g * 4;
-                    b[j] = (row_ok && k < K)
-                               ? *reinterpret_cast<const uint32_t*>(a.Aq + row * K + k)
-                               : 0u;
-                }
                 if constexpr (FP8) {
-                    bytes_to_bf16_op(b, xc[kb]);
+                    bytes_to_bf16_op(cur.c[kb], xc[kb]);
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) xc[kb][j] = b[j];
+                    for (int j = 0; j < 4; ++j) xc[kb][j] = cur.c[kb][j];
                 }
             }
             if constexpr (OUT == OUT_EPI) srow = row_ok ? a.scale_in[row] : 1.0f;
         } else {
-            float4 x[KB][4];
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k = kb * 64 + j * 16 + g * 4;
-                    x[kb][j] = (row_ok && k < K)
-                                   ? *reinterpret_cast<const float4*>(a.A + row * K + k)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
             float inv;
             if constexpr (IN == IN_F32_TOKEN) {
                 float mx = 0.0f;
@@ -305,10 +404,10 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
                 for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        mx = fmaxf(mx, fabsf(x[kb][j].x));
-                        mx = fmaxf(mx, fabsf(x[kb][j].y));
-                        mx = fmaxf(mx, fabsf(x[kb][j].z));
-                        mx = fmaxf(mx, fabsf(x[kb][j].w));
+                        mx = fmaxf(mx, fabsf(cur.x[kb][j][0]));
+                        mx = fmaxf(mx, fabsf(cur.x[kb][j][1]));
+                        mx = fmaxf(mx, fabsf(cur.x[kb][j][2]));
+                        mx = fmaxf(mx, fabsf(cur.x[kb][j][3]));
                     }
                 mx = fmaxf(mx, __shfl_xor(mx, 16));
                 mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -324,41 +423,63 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
                 srow = a.scale_A;
                 inv = FP8 ? ((srow == 0.0f) ? 1.0f : 1.0f / srow) : 0.0f;
             }
+            if constexpr (FP8) {
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
+                for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 v = x[kb][j];
-                    if constexpr (FP8) {
-                        xc[kb][2 * j] = bf16_bits(fp8_value(v.x, inv)) |
-                                        (bf16_bits(fp8_value(v.y, inv)) << 16);
-                        xc[kb][2 * j + 1] = bf16_bits(fp8_value(v.z, inv)) |
-                                            (bf16_bits(fp8_value(v.w, inv)) << 16);
-                    } else if constexpr (IN == IN_F32_TOKEN) {
-                        xc[kb][j] = pack4(quant_i8_token(v.x, srow, inv),
-                                          quant_i8_token(v.y, srow, inv),
-                                          quant_i8_token(v.z, srow, inv),
-                                          quant_i8_token(v.w, srow, inv));
-                    } else {
-                        xc[kb][j] = pack4(quant_i8_exact(v.x, srow, a.zp_A),
-                                          quant_i8_exact(v.y, srow, a.zp_A),
-                                          quant_i8_exact(v.z, srow, a.zp_A),
-                                          quant_i8_exact(v.w, srow, a.zp_A));
+                    for (int j = 0; j < 4; ++j) {
+                        const v4f v = cur.x[kb][j];
+                        xc[kb][2 * j] = bf16_bits(fp8_value(v[0], inv)) |
+                                        (bf16_bits(fp8_value(v[1], inv)) << 16);
+                        xc[kb][2 * j + 1] = bf16_bits(fp8_value(v[2], inv)) |
+                                            (bf16_bits(fp8_value(v[3], inv)) << 16);
+                    }
+            } else if constexpr (IN == IN_F32_TOKEN) {
+                // Reciprocal fast path for all elements, then one branch per
+                // lane that redoes the lane's codes exactly if any element
+                // was too close to a rounding tie.
+                bool slow = false;
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4f v = cur.x[kb][j];
+                        int32_t q0, q1, q2, q3;
+                        const bool ok = quant_i8_fast(v[0], inv, q0) & quant_i8_fast(v[1], inv, q1) &
+                                        quant_i8_fast(v[2], inv, q2) & quant_i8_fast(v[3], inv, q3);
+                        slow |= !ok;
+                        xc[kb][j] = pack4(q0, q1, q2, q3);
+                    }
+                if (slow) {
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) xc[kb][j] = pack4_token_exact(cur.x[kb][j], srow, inv);
+                }
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4f v = cur.x[kb][j];
+                        xc[kb][j] = pack4(quant_i8_exact(v[0], srow, a.zp_A),
+                                          quant_i8_exact(v[1], srow, a.zp_A),
+                                          quant_i8_exact(v[2], srow, a.zp_A),
+                                          quant_i8_exact(v[3], srow, a.zp_A));
                         // Padding beyond K must stay 0 even when zp_A != 0.
                         const int k = kb * 64 + j * 16 + g * 4;
                         if (!(row_ok && k < K)) xc[kb][j] = 0u;
                     }
-                }
+            }
         }
 
         int32_t SA = 0;
-        if constexpr (!FP8 && OUT == OUT_EPI) {
+        if constexpr (INT_EPI) {
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) SA = sum_bytes_i8(xc[kb][j], SA);
-            SA += __shfl_xor(SA, 16);
-            SA += __shfl_xor(SA, 32);
+            SA = row_sum4(SA);
         }
 
         if constexpr (HOIST) {
@@ -369,7 +490,15 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 #pragma unroll
                 for (int kb = 0; kb < KB; ++kb)
                     if (kb < kb_dot) mfma_block<FP8>(wh[nt][kb], xc[kb], acc_i, acc_f);
-                store_tile<FP8, ACT, OUT>(a, row, nt * 16, g, acc_i, acc_f, cch[nt], srow, SA);
+                IntEpi e[4];
+                if constexpr (INT_EPI) {
+                    if (!triv[nt]) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) e[v] = lds_e[nt * 16 + 4 * g + v];
+                    }
+                }
+                store_tile<FP8, ACT, OUT>(a, row, nt * 16, g, acc_i, acc_f, lds_sw[nt * 4 + g],
+                                          lds_b[nt * 4 + g], triv[nt], e, srow, SA);
             }
         } else {
             for (int n0 = 0; n0 < N; n0 += 64) {
@@ -384,7 +513,7 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
                     for (int kb = 0; kb < KB; ++kb) {
                         uint32_t w[DW];
                         int32_t ps;
-                        load_w_op<FP8>(a.W, K, N, nc, kb, r, g, w, ps);
+                        load_w_op<FP8, KFULL>(a.W, K, N, nc, kb, r, g, w, ps);
                         pf += ps;
                         if (kb < kb_dot) {
                             pd += ps;
@@ -392,8 +521,13 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
                         }
                     }
                     ColConsts cc;
-                    col_consts<FP8, OUT>(a, nc, g, pf, pd, cc);
-                    store_tile<FP8, ACT, OUT>(a, row, nc, g, acc_i, acc_f, cc, srow, SA);
+                    IntEpi mine, e[4];
+                    col_setup<FP8, OUT>(a, nc, r, g, pf, pd, cc, mine, true);
+                    if constexpr (INT_EPI) {
+                        if (!cc.trivial) gather_consts(mine, g, e);
+                    }
+                    store_tile<FP8, ACT, OUT>(a, row, nc, g, acc_i, acc_f, cc.sw, cc.b, cc.trivial, e,
+                                              srow, SA);
                 }
             }
         }

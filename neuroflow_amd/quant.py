@@ -375,6 +375,23 @@ class Int8Linear:
     def __call__(self, x: torch.Tensor, activation="gelu", out=None) -> torch.Tensor:
         return linear_forward_per_token(self.params, x, activation, out=out)
 
+    def launcher(self, activation="gelu"):
+        """A prepared call for a hot loop: `run(x_ptr, out_ptr, M, stream)`
+        with raw device pointers, the C struct built once.  The caller keeps
+        x / out alive and shaped (M, in_features) / (M, out_features)."""
+        ps = self.params.c_struct()
+        fn = _lib.lib().nflow_int8_linear_forward_per_token
+        ref = C.byref(ps)
+        act = _act(activation)
+
+        def run(x_ptr: int, out_ptr: int, M: int, stream: int) -> None:
+            rc = fn(ref, M, x_ptr, out_ptr, None, act, stream)
+            if rc:
+                check(rc, "linear_forward_per_token")
+
+        run.params = ps  # keep the struct alive with the closure
+        return run
+
 
 class Fp8Linear:
     """A per-channel symmetric FP8 E4M3 linear layer resident on the device."""
@@ -389,3 +406,18 @@ class Fp8Linear:
 
     def __call__(self, x: torch.Tensor, activation="gelu", out=None) -> torch.Tensor:
         return fp8_linear_forward_per_token(self.params, x, activation, out=out)
+
+    def launcher(self, activation="gelu"):
+        """Prepared hot-loop call, as Int8Linear.launcher."""
+        ps = self.params.c_struct()
+        fn = _lib.lib().nflow_fp8_linear_forward_per_token
+        ref = C.byref(ps)
+        act = _act(activation)
+
+        def run(x_ptr: int, out_ptr: int, M: int, stream: int) -> None:
+            rc = fn(ref, M, x_ptr, out_ptr, None, act, stream)
+            if rc:
+                check(rc, "fp8_linear_forward_per_token")
+
+        run.params = ps
+        return run
