@@ -29,7 +29,34 @@
 
 #include "common.h"
 
+// Cache policy of the streaming activation reads and output writes
+// (1 = non-temporal).
+#ifndef NFQ_NT_LOAD
+#define NFQ_NT_LOAD 0
+#endif
+#ifndef NFQ_NT_STORE
+#define NFQ_NT_STORE 0
+#endif
+
 namespace nfq {
+
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* p) {
+#if NFQ_NT_LOAD
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void stream_store(T v, T* p) {
+#if NFQ_NT_STORE
+    __builtin_nontemporal_store(v, p);
+#else
+    *p = v;
+#endif
+}
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
@@ -222,10 +249,10 @@ __device__ __forceinline__ void store_tile(const RowsArgs& a, int64_t row, int n
     if constexpr (OUT == OUT_RAW) {
         if constexpr (FP8) {
             if (nb < a.N)
-                __builtin_nontemporal_store(acc_f, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
+                stream_store(acc_f, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
         } else {
             if (nb < a.N)
-                __builtin_nontemporal_store(acc_i, reinterpret_cast<v4i*>(static_cast<int32_t*>(a.C) + row * a.N + nb));
+                stream_store(acc_i, reinterpret_cast<v4i*>(static_cast<int32_t*>(a.C) + row * a.N + nb));
         }
     } else {
         v4f t;
@@ -242,7 +269,7 @@ __device__ __forceinline__ void store_tile(const RowsArgs& a, int64_t row, int n
 #pragma unroll
         for (int v = 0; v < 4; ++v) y[v] = activate<ACT>(dequant_bias(sw[v], srow, t[v], bias[v]));
         if (nb < a.N)
-            __builtin_nontemporal_store(y, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
+            stream_store(y, reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * a.N + nb));
     }
 }
 
@@ -293,9 +320,9 @@ __device__ __forceinline__ void load_tile(const RowsArgs& a, int64_t tile, int r
             for (int j = 0; j < 4; ++j) {
                 const int k = kb * 64 + j * 16 + g * 4;
                 if constexpr (KFULL) {
-                    t.x[kb][j] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + k));
+                    t.x[kb][j] = stream_load(reinterpret_cast<const v4f*>(base + k));
                 } else {
-                    const v4f v = __builtin_nontemporal_load(
+                    const v4f v = stream_load(
                         reinterpret_cast<const v4f*>(base + (k < K ? k : K - 4)));
                     t.x[kb][j] = k < K ? v : v4f{0.f, 0.f, 0.f, 0.f};
                 }
