@@ -10,12 +10,14 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
 
 #include "../../include/nflow_quant.h"
 #include "common.h"
+#include "rows64_kernel.h"
 #include "rows_kernel.h"
 #include "status.h"
 
@@ -194,6 +196,13 @@ static unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_p
 
 static hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// A kernel-selection override read once per process (for A/B comparisons of
+// two kernels that compute the same bits).
+static bool getenv_flag(const char* name) {
+    const char* v = std::getenv(name);
+    return v && v[0] && v[0] != '0';
+}
+
 static bool aligned(const void* p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
@@ -267,6 +276,26 @@ static void launch_rows(const RowsArgs& a, int act, hipStream_t st) {
         else if (act == ACT_GELU_TANH) launch_rows_act<FP8, IN, OUT, ACT_GELU_TANH>(a, st);
         else launch_rows_act<FP8, IN, OUT, ACT_NONE>(a, st);
     }
+}
+
+// The K = N = 64 per-token layer (rows64_kernel.h).
+static bool rows64_ok(const RowsArgs& a) {
+    return a.K == 64 && a.N == 64 && aligned(a.A, 16) && aligned(a.C, 16) && aligned(a.W, 4);
+}
+
+template <bool FP8, int ACT>
+static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
+    auto kern = k_rows64<FP8, ACT>;
+    static const int per_cu = resident_blocks(kern);
+    const int64_t tiles = (a.M + 15) / 16;
+    hipLaunchKernelGGL(kern, dim3(grid_for(tiles, 4, per_cu)), dim3(256), 0, st, a);
+}
+
+template <bool FP8>
+static void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
+    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU>(a, st);
+    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH>(a, st);
+    else launch_rows64_act<FP8, ACT_NONE>(a, st);
 }
 
 template <bool FP8, int OUT>
@@ -440,6 +469,10 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
     a.kb_dot = kb_dot_for(a.formula, a.K);
     a.C = C;
     a.scale_out = scale_A_out;
+    if (rows64_ok(a) && !getenv_flag("NFLOW_NO_ROWS64")) {
+        launch_rows64<false>(a, activation, st);
+        return check_launch("linear_forward_per_token");
+    }
     if (rows_ok(a, IN_F32_TOKEN)) {
         launch_rows<false, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
         return check_launch("linear_forward_per_token");
@@ -575,6 +608,10 @@ int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t
     a.kb_dot = (a.K + 63) / 64;
     a.C = C;
     a.scale_out = scale_A_out;
+    if (rows64_ok(a) && !getenv_flag("NFLOW_NO_ROWS64")) {
+        launch_rows64<true>(a, activation, st);
+        return check_launch("fp8_linear_forward_per_token");
+    }
     if (rows_ok(a, IN_F32_TOKEN)) {
         launch_rows<true, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
         return check_launch("fp8_linear_forward_per_token");

@@ -162,3 +162,45 @@ def test_status_codes(gpu):
     with pytest.raises(NflowError) as ei:
         _lib.check(rc, "Int8Linear")
     assert ei.value.code == _lib.INVALID_ARG
+
+
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_fused_k64_layer_special_rows(gpu, act):
+    """The K = N = 64 fused layer on rows that exercise its exact slow path
+    (quotients on k + 0.5), zero rows, NaN / Inf and tiny values."""
+    M, K, N = 67, 64, 64
+    A = WL.normal(50, (M, K))
+    A[1] = 0.0
+    A[2, 0] = 127.0
+    A[2, 1:] = (np.arange(1, K, dtype=np.float32) - 32.0) * 0.5      # k + 0.5 ties
+    A[3, 0] = -127.0
+    A[3, 1:] = (np.arange(1, K, dtype=np.float32) * 0.5)
+    A[4, 5] = np.nan
+    A[5, 7] = np.inf
+    A[6] = 1e-30
+    A[7, :3] = [1e30, -1e30, 2.5]
+    _, q, s, zps, sw, b = _weights(N, K, 51)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw))
+    out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
+    ref, sa_ref = O.layer_per_token_i8(A, q, s, zps, b, sw, {"none": 0, "gelu": 2}[act])
+    out = _host(out)
+    assert _bits_equal(_host(sa), sa_ref)
+    if act == "none":
+        finite = np.isfinite(ref)
+        assert _bits_equal(out[finite], ref[finite])
+        assert np.array_equal(np.isnan(out), np.isnan(ref))
+    else:
+        np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+
+
+def test_fused_k64_layer_asymmetric_weights(gpu):
+    """Zero points in the K = N = 64 fused layer reproduce LinearForward's formula."""
+    M, K, N = 300, 64, 64
+    A = WL.normal(52, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 53, zp=True)
+    for sumW in (None, sw):
+        p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b),
+                               sum_W_per_row=None if sumW is None else _cu(sumW))
+        out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
+        ref, _ = O.layer_per_token_i8(A, q, s, zps, b, sumW, 0)
+        assert _bits_equal(out, ref)
