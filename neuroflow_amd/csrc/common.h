@@ -13,6 +13,7 @@
 namespace nfq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 enum Act { ACT_NONE = 0, ACT_RELU = 1, ACT_GELU_TANH = 2 };
@@ -139,20 +140,26 @@ __device__ __forceinline__ uint32_t fp8_quant(float x, float inv) {
 //   |xc| <  2^-6  multiples of 2^-9 with ties to even, capped at 7 * 2^-9
 //                 (fp8_e4m3.h:192-211): (|xc| + 2^14) - 2^14 rounds to the
 //                 2^-9 grid because ulp(2^14) = 2^-9.
-__device__ __forceinline__ float fp8_value(float x, float inv) {
-    const float xs = x * inv;
-    if (__builtin_isnan(xs)) return xs;
-    const float xc = (xs > 448.0f) ? 448.0f : ((xs < -448.0f) ? -448.0f : xs);
+__device__ __forceinline__ float fp8_value_of(float xs) {
+    const float xc = __builtin_amdgcn_fmed3f(xs, -448.0f, 448.0f);  // xs not NaN
     const uint32_t u = __float_as_uint(xc);
-    const uint32_t mag = u & 0x7FFFFFFFu;
     const uint32_t nrm = (u + 0x7FFFFu + ((u >> 20) & 1u)) & 0xFFF00000u;
-    const float sub = fminf((__uint_as_float(mag) + 0x1p14f) - 0x1p14f, 7.0f * 0x1p-9f);
+    const float sub = fminf((fabsf(xc) + 0x1p14f) - 0x1p14f, 7.0f * 0x1p-9f);
     const uint32_t subb = __float_as_uint(sub) | (u & 0x80000000u);
-    return __uint_as_float(mag < 0x3C800000u ? subb : nrm);
+    return __uint_as_float(fabsf(xc) < 0x1p-6f ? subb : nrm);
 }
 
-// bfloat16 bits of an E4M3 value held as fp32 (exact: at most 4 significant bits).
-__device__ __forceinline__ uint32_t bf16_bits(float v) { return __float_as_uint(v) >> 16; }
+__device__ __forceinline__ float fp8_value(float x, float inv) {
+    const float xs = x * inv;
+    const float v = fp8_value_of(xs);
+    return __builtin_isnan(xs) ? xs : v;
+}
+
+// bfloat16 bits of two E4M3 values held as fp32, low half first (one v_perm).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
 
 // bfloat16 bits of the E4M3 byte b (the value of e4m3_decode, exactly).
 __device__ __forceinline__ uint32_t e4m3_to_bf16(uint32_t b) {

@@ -1,0 +1,82 @@
+// launch.h -- host-side launch helpers and the launcher declarations shared
+// by the translation units of libnflow_quant (one unit per kernel family, so
+// the device code of each compiles in parallel).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <mutex>
+
+#include "../../include/nflow_quant.h"
+#include "rows_kernel.h"
+
+namespace nfq {
+
+inline int num_cus() {
+    static int cached = 0;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached == 0) {
+        int dev = 0;
+        int cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            cu > 0)
+            cached = cu;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
+inline unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_per_cu) {
+    const int64_t want = (work_items + per_block - 1) / per_block;
+    const int64_t cap = static_cast<int64_t>(num_cus()) * max_blocks_per_cu;
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min(want, cap)));
+}
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// A kernel-selection override read once per process (for A/B comparisons of
+// two kernels that compute the same bits).
+inline bool getenv_flag(const char* name) {
+    const char* v = std::getenv(name);
+    return v && v[0] && v[0] != '0';
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+// Row-tile kernel eligibility for the given input mode.
+inline bool rows_ok(const RowsArgs& a, int in_mode) {
+    if (a.K % 4 != 0 || a.N % 4 != 0) return false;
+    if (in_mode == IN_CODES) {
+        if (a.K > 1024 || !aligned(a.Aq, 4)) return false;
+    } else {
+        if (a.K > 256 || !aligned(a.A, 16)) return false;
+    }
+    return aligned(a.W, 4) && aligned(a.C, 16);
+}
+
+// Resident blocks per CU of a kernel (cached per instantiation).
+template <typename Kernel>
+inline int resident_blocks(Kernel k) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, 0) != hipSuccess || n < 1) n = 1;
+    return n;
+}
+
+// Row-tile kernel launchers, explicitly instantiated in rows_*.hip.
+template <bool FP8, int IN, int OUT>
+void launch_rows(const RowsArgs& a, int act, hipStream_t st);
+
+// The K = N = 64 per-token layer (rows64.hip).
+bool rows64_ok(const RowsArgs& a);
+template <bool FP8>
+void launch_rows64(const RowsArgs& a, int act, hipStream_t st);
+
+}  // namespace nfq

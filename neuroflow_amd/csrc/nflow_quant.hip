@@ -17,7 +17,7 @@
 
 #include "../../include/nflow_quant.h"
 #include "common.h"
-#include "rows64_kernel.h"
+#include "launch.h"
 #include "rows_kernel.h"
 #include "status.h"
 
@@ -170,133 +170,6 @@ __global__ __launch_bounds__(256) void k_generic(RowsArgs a, int act) {
 // ---------------------------------------------------------------------------
 // Launch helpers
 // ---------------------------------------------------------------------------
-
-static int num_cus() {
-    static int cached = 0;
-    static std::mutex mu;
-    std::lock_guard<std::mutex> lock(mu);
-    if (cached == 0) {
-        int dev = 0;
-        int cu = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            cu > 0)
-            cached = cu;
-        else
-            cached = 256;
-    }
-    return cached;
-}
-
-static unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_per_cu) {
-    const int64_t want = (work_items + per_block - 1) / per_block;
-    const int64_t cap = static_cast<int64_t>(num_cus()) * max_blocks_per_cu;
-    return static_cast<unsigned>(std::max<int64_t>(1, std::min(want, cap)));
-}
-
-static hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
-
-// A kernel-selection override read once per process (for A/B comparisons of
-// two kernels that compute the same bits).
-static bool getenv_flag(const char* name) {
-    const char* v = std::getenv(name);
-    return v && v[0] && v[0] != '0';
-}
-
-static bool aligned(const void* p, uintptr_t a) {
-    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
-}
-
-// Row-tile kernel eligibility for the given input mode.
-static bool rows_ok(const RowsArgs& a, int in_mode) {
-    if (a.K % 4 != 0 || a.N % 4 != 0) return false;
-    if (in_mode == IN_CODES) {
-        if (a.K > 1024 || !aligned(a.Aq, 4)) return false;
-    } else {
-        if (a.K > 256 || !aligned(a.A, 16)) return false;
-    }
-    return aligned(a.W, 4) && aligned(a.C, 16);
-}
-
-// Resident blocks per CU of a kernel (cached per instantiation).
-template <typename Kernel>
-static int resident_blocks(Kernel k) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, 0) != hipSuccess || n < 1) n = 1;
-    return n;
-}
-
-// Persistent launch: one wave per resident slot, each looping over row tiles.
-template <int KB, bool FP8, int IN, int OUT, int ACT, bool HOIST, bool KFULL>
-static void launch_rows_k(const RowsArgs& a, hipStream_t st) {
-    auto kern = k_rows<KB, FP8, IN, OUT, ACT, HOIST, KFULL>;
-    static const int per_cu = resident_blocks(kern);
-    const int64_t tiles = (a.M + 15) / 16;
-    const unsigned grid = grid_for(tiles, 4, per_cu);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
-}
-
-template <int KB, bool FP8, int IN, int OUT, int ACT, bool KFULL>
-static void launch_rows_h(const RowsArgs& a, hipStream_t st) {
-    if constexpr (rows_hoist_fits(KB, FP8)) {
-        if (a.N <= 64) {
-            launch_rows_k<KB, FP8, IN, OUT, ACT, true, KFULL>(a, st);
-            return;
-        }
-    }
-    launch_rows_k<KB, FP8, IN, OUT, ACT, false, KFULL>(a, st);
-}
-
-template <int KB, bool FP8, int IN, int OUT, int ACT>
-static void launch_rows_kb(const RowsArgs& a, hipStream_t st) {
-    // The fixed-scale paths (LinearForward / LinearForwardBatched) are not
-    // the hot loop: one instantiation with range checks serves every K.
-    if (IN != IN_F32_FIXED && a.K == KB * 64) launch_rows_h<KB, FP8, IN, OUT, ACT, true>(a, st);
-    else launch_rows_h<KB, FP8, IN, OUT, ACT, false>(a, st);
-}
-
-template <bool FP8, int IN, int OUT, int ACT>
-static void launch_rows_act(const RowsArgs& a, hipStream_t st) {
-    const int kb = (a.K + 63) / 64;
-    if (kb <= 1) launch_rows_kb<1, FP8, IN, OUT, ACT>(a, st);
-    else if (kb <= 2) launch_rows_kb<2, FP8, IN, OUT, ACT>(a, st);
-    else if (kb <= 4) launch_rows_kb<4, FP8, IN, OUT, ACT>(a, st);
-    else if constexpr (IN == IN_CODES) {
-        if (kb <= 8) launch_rows_kb<8, FP8, IN, OUT, ACT>(a, st);
-        else launch_rows_kb<16, FP8, IN, OUT, ACT>(a, st);
-    }
-}
-
-template <bool FP8, int IN, int OUT>
-static void launch_rows(const RowsArgs& a, int act, hipStream_t st) {
-    if constexpr (OUT == OUT_RAW) {
-        launch_rows_act<FP8, IN, OUT, ACT_NONE>(a, st);
-    } else {
-        if (act == ACT_RELU) launch_rows_act<FP8, IN, OUT, ACT_RELU>(a, st);
-        else if (act == ACT_GELU_TANH) launch_rows_act<FP8, IN, OUT, ACT_GELU_TANH>(a, st);
-        else launch_rows_act<FP8, IN, OUT, ACT_NONE>(a, st);
-    }
-}
-
-// The K = N = 64 per-token layer (rows64_kernel.h).
-static bool rows64_ok(const RowsArgs& a) {
-    return a.K == 64 && a.N == 64 && aligned(a.A, 16) && aligned(a.C, 16) && aligned(a.W, 4);
-}
-
-template <bool FP8, int ACT>
-static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
-    auto kern = k_rows64<FP8, ACT>;
-    static const int per_cu = resident_blocks(kern);
-    const int64_t tiles = (a.M + 15) / 16;
-    hipLaunchKernelGGL(kern, dim3(grid_for(tiles, 4, per_cu)), dim3(256), 0, st, a);
-}
-
-template <bool FP8>
-static void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
-    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU>(a, st);
-    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH>(a, st);
-    else launch_rows64_act<FP8, ACT_NONE>(a, st);
-}
 
 template <bool FP8, int OUT>
 static void launch_generic(const RowsArgs& a, int act, hipStream_t st) {

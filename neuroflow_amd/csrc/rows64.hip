@@ -1,0 +1,45 @@
+// rows64.hip -- launchers of the K = N = 64 per-token layer (rows64_kernel.h).
+#include "launch.h"
+#include "rows64_kernel.h"
+
+namespace nfq {
+
+// The K = N = 64 per-token layer (rows64_kernel.h).
+bool rows64_ok(const RowsArgs& a) {
+    return a.K == 64 && a.N == 64 && aligned(a.A, 16) && aligned(a.C, 16) && aligned(a.W, 4);
+}
+
+// Tiles of 16 rows each loaded this many tiles ahead by every wave.
+#ifndef NFQ_ROWS64_PF
+#define NFQ_ROWS64_PF 1
+#endif
+
+template <bool FP8, int ACT>
+static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
+    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF>;
+    static const int per_cu = resident_blocks(kern);
+    // Persistent waves that all take the same number of tiles (to within
+    // one): the fewest waves that keep the per-wave count of a full grid.
+    const int64_t tiles = (a.M + 15) / 16;
+#ifdef NFQ_ROWS64_TILES_PER_WAVE
+    const int64_t per_wave = NFQ_ROWS64_TILES_PER_WAVE;
+    (void)per_cu;
+#else
+    const int64_t slots = static_cast<int64_t>(num_cus()) * per_cu * 4;
+    const int64_t per_wave = (tiles + slots - 1) / slots;
+#endif
+    const int64_t waves = (tiles + per_wave - 1) / per_wave;
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, st, a);
+}
+
+template <bool FP8>
+void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
+    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU>(a, st);
+    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH>(a, st);
+    else launch_rows64_act<FP8, ACT_NONE>(a, st);
+}
+
+template void launch_rows64<false>(const RowsArgs&, int, hipStream_t);
+template void launch_rows64<true>(const RowsArgs&, int, hipStream_t);
+
+}  // namespace nfq

@@ -29,8 +29,11 @@ __device__ __forceinline__ float dpp_mov(float v) {
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-// Max over the 16 lanes of a DPP row (NaN operands are ignored by fmaxf).
-__device__ __forceinline__ float row16_max(float v) {
+// Absmax over the 16 lanes of a DPP row of four-float chunks, NaN operands
+// ignored and starting from 0 (the reference's `if (a > m) m = a` loop):
+// fmaxf, so every step canonicalises.  The exact path uses it.
+__device__ __forceinline__ float row16_absmax_exact(v4f x) {
+    float v = fmaxf(fmaxf(fmaxf(0.0f, fabsf(x[0])), fmaxf(fabsf(x[1]), fabsf(x[2]))), fabsf(x[3]));
     v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
     v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
     v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
@@ -38,24 +41,39 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
+// The same reduction as six VALU instructions: VOP3 max3 with |.| modifiers
+// from 0, then max with a DPP-moved operand (the compiler would add a
+// canonicalising max per DPP move).  IEEE-mode max returns the other operand
+// for a quiet NaN, so the result equals row16_absmax_exact unless the row
+// holds a signalling NaN, in which case it is NaN and the caller takes the
+// exact path.  s_nop 1 covers the VALU-write -> DPP-read hazard.
+__device__ __forceinline__ float row16_absmax_fast(v4f x) {
+    float m;
+    asm("v_max3_f32 %0, |%1|, |%2|, 0\n\t"
+        "v_max3_f32 %0, %0, |%3|, |%4|\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf"
+        : "=&v"(m)
+        : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+    return m;
+}
+
 __device__ __forceinline__ float bperm_f(int src_lane, float v) {
     return __builtin_bit_cast(float,
                               __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
 }
 
-// Exact per-token INT8 codes of four elements of a row whose absmax is amax
-// (the rare slow path; out of line so the hot loop does not carry it).
-__device__ __attribute__((noinline)) uint32_t pack4_token_exact_amax(v4f v, float amax) {
-    const float s = (amax == 0.0f) ? 1.0f : amax / 127.0f;
-    const float inv = 1.0f / s;
-    return pack4(quant_i8_token(v[0], s, inv), quant_i8_token(v[1], s, inv),
-                 quant_i8_token(v[2], s, inv), quant_i8_token(v[3], s, inv));
-}
-
-// Per-wave LDS: codes (row stride padded against bank conflicts) and the
-// output tile (row stride 68 floats).
+// Per-wave LDS: the operand codes (row stride padded against bank
+// conflicts) and the output tile (row stride 68 floats) share one buffer --
+// the codes are in registers before the first output value is written.
 template <bool FP8>
-struct alignas(16) Rows64Lds {
+union alignas(16) Rows64Lds {
     static constexpr int CODE_DW = FP8 ? 32 : 16;        // dwords of one row's operand data
     static constexpr int CODE_STRIDE = CODE_DW + 4;      // padded
     static constexpr int OUT_STRIDE = 68;                // floats
@@ -63,89 +81,146 @@ struct alignas(16) Rows64Lds {
     float out[16 * OUT_STRIDE];
 };
 
-template <bool FP8, int ACT>
+// FP8 weights as the bf16 MFMA operand, shared by the block: row n holds
+// W[n][0..63] (32 dwords) with a stride of 36 dwords, so the 8 lanes of a
+// ds_read_b128 phase (rows r .. r + 7) fall in distinct banks.
+constexpr int W_BF16_STRIDE = 36;
+
+// Buffer resource over the 16-row tile starting at row0 of a row-major array
+// of M rows of row_bytes bytes.  The hardware range check returns zeros for
+// loads past row M - 1 and drops stores there, so partial and past-the-end
+// tiles need no branches.  row0 must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, int64_t row0,
+                                                            int64_t M, int row_bytes) {
+    int64_t left = M - row0;
+    left = left < 0 ? 0 : (left > 16 ? 16 : left);
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(base)) + row0 * row_bytes, 0,
+        static_cast<int>(left) * row_bytes, 0x00020000);
+}
+
+// Per-token INT8 code of t = a * inv_s for the fast path, and whether it may
+// differ from the reference's.  With s = fl(amax / 127) normal, |a| <= amax
+// and inv_s within 1 ulp of 1 / s (v_rcp_f32), t differs from q = fl(a / s)
+// by at most 2^-22 |t|, and |t| < 127.5.  If the distance of t from
+// r = rint(t) (exact: t and r are within a factor 2) is below
+// 0.5 - 2^-21 |t|, q is closer than 0.5 to r, so round-half-away(q) == r and
+// no clamp is needed.  NaN / Inf elements give a NaN distance and fail.
+__device__ __forceinline__ int32_t quant_i8_near(float a, float inv_s, uint64_t& slow) {
+    const float t = a * inv_s;
+    const float r = rintf(t);
+    const float lim = __builtin_fmaf(fabsf(t), -0x1p-21f, 0.5f);
+    slow |= __builtin_amdgcn_ballot_w64(!(fabsf(t - r) < lim));
+    return static_cast<int32_t>(r);
+}
+
+// A row takes the exact path when its fast absmax is NaN (a signalling NaN
+// in the row) or, for INT8, when amax / 127 would be subnormal (t may then
+// leave the int8 range).
+template <bool FP8>
+__device__ __forceinline__ bool amax_needs_exact(float amax) {
+    if constexpr (FP8) return amax != amax;
+    return !(amax == 0.0f || (amax >= 0x1p-119f && amax <= 0x1.fffffep+127f));
+}
+
+// Exact per-token INT8 codes of four elements with scale s (the reference's
+// correctly rounded quotient and half-away rounding).
+__device__ __attribute__((noinline)) uint32_t pack4_token_scale(v4f v, float s) {
+    const float inv = 1.0f / s;
+    return pack4(quant_i8_token(v[0], s, inv), quant_i8_token(v[1], s, inv),
+                 quant_i8_token(v[2], s, inv), quant_i8_token(v[3], s, inv));
+}
+
+template <bool FP8, int ACT, int PF = 1>
 __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     constexpr bool INT_EPI = !FP8;
     using L = Rows64Lds<FP8>;
     const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;       // MFMA layout
     const int g = lane >> 4;
     const int lr = lane >> 4;      // linear layout: row within a 4-row group
-    const int lc = lane & 15;      //                4-float column chunk
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
     const int64_t ntiles = (a.M + 15) >> 4;
     const int64_t M = a.M;
+    const int lin_off = lane * 16;  // byte offset of the lane in a 4-row group
+    constexpr int DW = FP8 ? 8 : 4;  // operand dwords per lane
 
     __shared__ L lds[4];
     __shared__ IntEpi lds_e[INT_EPI ? 64 : 1];
+    __shared__ uint32_t lds_w[FP8 ? 64 * W_BF16_STRIDE : 1];
     __shared__ v4f lds_sw[16];
     __shared__ v4f lds_b[16];
     L& my = lds[wid];
 
-    // Linear-layout load of one tile (rows past M re-read row M-1 and are
-    // never stored).
-    auto load_lin = [&](int64_t tile, v4f (&x)[4]) {
+    // Linear-layout load of one tile: instruction j reads rows 4j .. 4j + 3.
+    auto load_lin = [&](int64_t t, v4f (&x)[4]) {
+        const auto rs = tile_rsrc(a.A, t * 16, M, 256);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int64_t row = tile * 16 + 4 * j + lr;
-            row = row < M ? row : M - 1;
-            x[j] = *reinterpret_cast<const v4f*>(a.A + row * 64 + 4 * lc);
-        }
+        for (int j = 0; j < 4; ++j)
+            x[j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, lin_off + 1024 * j, 0, 0));
     };
 
     int64_t tile = wave;
-    v4f nxt[4];
-    if (tile < ntiles) load_lin(tile, nxt);
+    v4f pre[PF][4];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load_lin(tile + p * nwaves, pre[p]);
 
-    // Weights: lane (r, g) holds W[16nt + r][16g .. 16g + 15] for nt = 0..3.
-    constexpr int DW = FP8 ? 8 : 4;
-    uint32_t wop[4][DW];
-    bool triv[4];
     if (threadIdx.x < 64) {
         const int n = threadIdx.x;
         reinterpret_cast<float*>(lds_sw)[n] = a.sW[n];
         reinterpret_cast<float*>(lds_b)[n] = a.bias ? a.bias[n] : 0.0f;
     }
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (16 * nt + r) * 64 + 16 * g);
-        uint32_t b[4];
+    // INT8 weights stay in registers: lane (r, g) holds W[16nt + r][16g ..
+    // 16g + 15] for nt = 0..3.  FP8 weights go to LDS as bf16 (thread t
+    // converts W[t / 4][16 (t % 4) .. + 15]).
+    uint32_t wi8[4][4];
+    bool triv[4] = {true, true, true, true};
+    if constexpr (FP8) {
+        const int n = threadIdx.x >> 2, c = threadIdx.x & 3;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + n * 64 + 16 * c);
+        uint32_t b[4], o[8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) b[q] = src[q];
-        int32_t ps = 0;
-        if constexpr (FP8) {
-            bytes_to_bf16_op(b, wop[nt]);
-        } else {
+        bytes_to_bf16_op(b, o);
+        v4u* dst = reinterpret_cast<v4u*>(lds_w + n * W_BF16_STRIDE + 8 * c);
+        dst[0] = v4u{o[0], o[1], o[2], o[3]};
+        dst[1] = v4u{o[4], o[5], o[6], o[7]};
+    } else {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (16 * nt + r) * 64 + 16 * g);
+            int32_t ps = 0;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                wop[nt][q] = b[q];
-                ps = sum_bytes_i8(b[q], ps);
+                wi8[nt][q] = src[q];
+                ps = sum_bytes_i8(wi8[nt][q], ps);
             }
-        }
-        IntEpi mine;
-        ColConsts cc;
-        col_setup<FP8, OUT_EPI>(a, 16 * nt, r, g, ps, ps, cc, mine, false);
-        triv[nt] = cc.trivial;
-        if constexpr (INT_EPI) {
+            IntEpi mine;
+            ColConsts cc;
+            col_setup<false, OUT_EPI>(a, 16 * nt, r, g, ps, ps, cc, mine, false);
+            triv[nt] = cc.trivial;
             if (wid == 0 && g == 0) lds_e[16 * nt + r] = mine;
         }
     }
+    const bool all_triv = triv[0] & triv[1] & triv[2] & triv[3];
     __syncthreads();
 
     for (; tile < ntiles; tile += nwaves) {
         v4f x[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = nxt[j];
-        if (tile + nwaves < ntiles) load_lin(tile + nwaves, nxt);
+        for (int j = 0; j < 4; ++j) x[j] = pre[0][j];
+#pragma unroll
+        for (int p = 0; p + 1 < PF; ++p)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pre[p][j] = pre[p + 1][j];
+        load_lin(tile + PF * nwaves, pre[PF - 1]);
 
         // Row absmax in the linear layout: amax[j] = absmax of row 4j + lr.
         float amax[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            amax[j] = row16_max(fmaxf(fmaxf(fabsf(x[j][0]), fabsf(x[j][1])),
-                                      fmaxf(fabsf(x[j][2]), fabsf(x[j][3]))));
+        for (int j = 0; j < 4; ++j) amax[j] = row16_absmax_fast(x[j]);
 
         // Row r's absmax to the MFMA-layout lanes (row r = 4j + q lives in
         // lanes 16q.. of amax[j]); scale and reciprocal once per row.
@@ -155,44 +230,94 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             const float v = bperm_f((r & 3) * 16, amax[j]);
             am_r = ((r >> 2) == j) ? v : am_r;
         }
+        uint64_t slow = __builtin_amdgcn_ballot_w64(amax_needs_exact<FP8>(am_r));
         const float qmax = FP8 ? 448.0f : 127.0f;
-        const float s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
-        const float inv_r = FP8 ? ((s_r == 0.0f) ? 1.0f : 1.0f / s_r) : 1.0f / s_r;
-        const int64_t row_r = tile * 16 + r;
-        if (a.scale_out && g == 0 && row_r < M) a.scale_out[row_r] = s_r;
+        float s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
+        // FP8 scales down by the correctly rounded 1 / s, as the reference.
+        float inv_r = FP8 ? ((s_r == 0.0f) ? 1.0f : 1.0f / s_r) : __builtin_amdgcn_rcpf(s_r);
 
         // Back to the linear layout: inverse scale of row 4j + lr.
         float inv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) inv[j] = bperm_f(4 * j + lr, inv_r);
 
-        // Quantise in the linear layout and stage the operand in LDS.
+        // Quantise in the linear layout.
+        const int lc = lane & 15;
+        uint32_t q[FP8 ? 8 : 4];
         if constexpr (FP8) {
+            // Fast path: no NaN among x * inv (a NaN sets the mask; the
+            // reference's NaN byte makes the whole output row NaN).
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t lo = bf16_bits(fp8_value(x[j][0], inv[j])) |
-                                    (bf16_bits(fp8_value(x[j][1], inv[j])) << 16);
-                const uint32_t hi = bf16_bits(fp8_value(x[j][2], inv[j])) |
-                                    (bf16_bits(fp8_value(x[j][3], inv[j])) << 16);
-                uint32_t* dst = my.codes + (4 * j + lr) * L::CODE_STRIDE + 2 * lc;
-                dst[0] = lo;
-                dst[1] = hi;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xs = x[j][e] * inv[j];
+                    slow |= __builtin_amdgcn_ballot_w64(__builtin_isnan(xs));
+                    v[e] = fp8_value_of(xs);
+                }
+                q[2 * j] = pack_bf16x2(v[0], v[1]);
+                q[2 * j + 1] = pack_bf16x2(v[2], v[3]);
+            }
+            if (slow) {
+                // A NaN element or a signalling NaN in the absmax: the
+                // canonical reduction, its scales and NaN-propagating values.
+#pragma unroll
+                for (int j = 0; j < 4; ++j) amax[j] = row16_absmax_exact(x[j]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float v = bperm_f((r & 3) * 16, amax[j]);
+                    am_r = ((r >> 2) == j) ? v : am_r;
+                }
+                s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
+                inv_r = (s_r == 0.0f) ? 1.0f : 1.0f / s_r;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) inv[j] = bperm_f(4 * j + lr, inv_r);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    q[2 * j] = pack_bf16x2(fp8_value(x[j][0], inv[j]), fp8_value(x[j][1], inv[j]));
+                    q[2 * j + 1] = pack_bf16x2(fp8_value(x[j][2], inv[j]), fp8_value(x[j][3], inv[j]));
+                }
             }
         } else {
-            uint32_t q[4];
-            bool slow = false;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                int32_t q0, q1, q2, q3;
-                const bool ok = quant_i8_fast(x[j][0], inv[j], q0) & quant_i8_fast(x[j][1], inv[j], q1) &
-                                quant_i8_fast(x[j][2], inv[j], q2) & quant_i8_fast(x[j][3], inv[j], q3);
-                slow |= !ok;
+                const int32_t q0 = quant_i8_near(x[j][0], inv[j], slow);
+                const int32_t q1 = quant_i8_near(x[j][1], inv[j], slow);
+                const int32_t q2 = quant_i8_near(x[j][2], inv[j], slow);
+                const int32_t q3 = quant_i8_near(x[j][3], inv[j], slow);
                 q[j] = pack4(q0, q1, q2, q3);
             }
             if (slow) {
+                // Exact path for the whole tile (wave-uniform branch): the
+                // canonical absmax, correctly rounded scales, exact codes.
 #pragma unroll
-                for (int j = 0; j < 4; ++j) q[j] = pack4_token_exact_amax(x[j], amax[j]);
+                for (int j = 0; j < 4; ++j) amax[j] = row16_absmax_exact(x[j]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float v = bperm_f((r & 3) * 16, amax[j]);
+                    am_r = ((r >> 2) == j) ? v : am_r;
+                }
+                s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) q[j] = pack4_token_scale(x[j], bperm_f(4 * j + lr, s_r));
             }
+        }
+        if (a.scale_out) {
+            // Every lane of row r stores the same value; rows >= M are dropped.
+            const auto rs = tile_rsrc(a.scale_out, tile * 16, M, 4);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_r), rs, r * 4, 0, 0);
+        }
+
+        // Stage the operand in LDS.
+        if constexpr (FP8) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t* dst = my.codes + (4 * j + lr) * L::CODE_STRIDE + 2 * lc;
+                dst[0] = q[2 * j];
+                dst[1] = q[2 * j + 1];
+            }
+        } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) my.codes[(4 * j + lr) * L::CODE_STRIDE + lc] = q[j];
         }
@@ -215,16 +340,31 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         }
         int32_t SA = 0;
         if constexpr (INT_EPI) {
+            if (!all_triv) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) SA = sum_bytes_i8(xo[q], SA);
-            SA = row_sum4(SA);
+                for (int q = 0; q < 4; ++q) SA = sum_bytes_i8(xo[q], SA);
+                SA = row_sum4(SA);
+            }
         }
 
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             v4i acc_i = {0, 0, 0, 0};
             v4f acc_f = {0.f, 0.f, 0.f, 0.f};
-            mfma_block<FP8>(wop[nt], xo, acc_i, acc_f);
+            uint32_t w[DW];
+            if constexpr (FP8) {
+                const v4u* src = reinterpret_cast<const v4u*>(lds_w + (16 * nt + r) * W_BF16_STRIDE + 8 * g);
+                const v4u w0 = src[0], w1 = src[1];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    w[q] = w0[q];
+                    w[4 + q] = w1[q];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) w[q] = wi8[nt][q];
+            }
+            mfma_block<FP8>(w, xo, acc_i, acc_f);
             v4f t;
             if constexpr (FP8) {
                 t = acc_f;
@@ -247,12 +387,14 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         // Linear-layout stores: rows 4j .. 4j + 3 whole per instruction.
+        v4f y[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t row = tile * 16 + 4 * j + lr;
-            const v4f y = *reinterpret_cast<const v4f*>(my.out + (4 * j + lr) * L::OUT_STRIDE + 4 * lc);
-            if (row < M) *reinterpret_cast<v4f*>(static_cast<float*>(a.C) + row * 64 + 4 * lc) = y;
-        }
+        for (int j = 0; j < 4; ++j)
+            y[j] = *reinterpret_cast<const v4f*>(my.out + (4 * j + lr) * L::OUT_STRIDE + 4 * lc);
+        const auto rs = tile_rsrc(a.C, tile * 16, M, 256);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, y[j]), rs, lin_off + 1024 * j, 0, 0);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }

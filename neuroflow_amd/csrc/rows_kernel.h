@@ -456,10 +456,8 @@ __global__ __launch_bounds__(256, rows_min_waves(KB, FP8)) void k_rows(RowsArgs 
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const v4f v = cur.x[kb][j];
-                        xc[kb][2 * j] = bf16_bits(fp8_value(v[0], inv)) |
-                                        (bf16_bits(fp8_value(v[1], inv)) << 16);
-                        xc[kb][2 * j + 1] = bf16_bits(fp8_value(v[2], inv)) |
-                                            (bf16_bits(fp8_value(v[3], inv)) << 16);
+                        xc[kb][2 * j] = pack_bf16x2(fp8_value(v[0], inv), fp8_value(v[1], inv));
+                        xc[kb][2 * j + 1] = pack_bf16x2(fp8_value(v[2], inv), fp8_value(v[3], inv));
                     }
             } else if constexpr (IN == IN_F32_TOKEN) {
                 // Reciprocal fast path for all elements, then one branch per

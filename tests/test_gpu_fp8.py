@@ -102,3 +102,32 @@ def test_fp8_layer(gpu, M, N, K, act):
         own = K * 2.0 ** -24 * (terms + np.abs(b)[None, :])
         assert np.all(np.abs(out.astype(np.float64) - composed) <=
                       ATOL + RTOL * np.abs(composed) + own)
+
+
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_fp8_layer_k64_special_rows(gpu, act):
+    """The K = N = 64 FP8 layer on zero, NaN (quiet, signalling, whole row),
+    infinite, subnormal and huge rows: scales bit-exact, NaN positions equal,
+    finite outputs within 1e-5 / 1e-6 of the exact-product oracle."""
+    M, K, N = 70, 64, 64
+    x = (2.0 * WL.normal(38, (M, K))).astype(np.float32)
+    x[1] = 0.0
+    x[2] = np.nan
+    x[3, :4] = np.nan
+    x.view(np.uint32)[4, 9] = 0x7F800001  # signalling NaN
+    x[5, 2] = np.inf
+    x[6] = 1e-40
+    x[7, :2] = [3e38, -3e38]
+    x[8] = -0.0
+    W = WL.uniform(39, (N, K), -0.125, 0.125)
+    b = WL.uniform(40, (N,), -0.125, 0.125)
+    layer = Q.Fp8Linear(W, b)
+    out, sa = Q.fp8_linear_forward_per_token(layer.params, _cu(x), act, return_scales=True)
+    out, sa = _host(out), _host(sa)
+    a = {"none": 0, "gelu": 2}[act]
+    qa, sa_ref = O.quantise_per_token_fp8(x)
+    assert np.array_equal(sa.view(np.uint32), sa_ref.view(np.uint32))
+    exact = O.layer_fp8_exact(qa, sa_ref, layer.W_q, layer.scale_W, b, a)
+    assert np.array_equal(np.isnan(out), np.isnan(exact))
+    fin = ~np.isnan(exact)
+    np.testing.assert_allclose(out[fin], exact[fin], rtol=RTOL, atol=ATOL)

@@ -179,6 +179,13 @@ def test_fused_k64_layer_special_rows(gpu, act):
     A[5, 7] = np.inf
     A[6] = 1e-30
     A[7, :3] = [1e30, -1e30, 2.5]
+    A[8] = np.nan                                   # every element NaN: scale 1
+    A[9, :4] = np.nan                               # one lane's whole chunk NaN
+    A.view(np.uint32)[10, 3] = 0x7F800001          # signalling NaN
+    A[11] = -0.0
+    A[12] = 1e-40                                   # subnormal absmax
+    A[13, :] *= 3e-37 / np.abs(A[13]).max()         # normal absmax, subnormal scale
+    A[14] = -np.inf
     _, q, s, zps, sw, b = _weights(N, K, 51)
     p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw))
     out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
