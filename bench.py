@@ -56,6 +56,20 @@ def parse():
     return ap.parse_args()
 
 
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload` from its committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each
+    scaled by what the counter reads for a plain streaming kernel of known
+    size), or None when no summary exists for that pair."""
+    f = ROOT / "profiles" / f"{kernel.split('::')[-1]}_{workload}_counters.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def build_layers(wl, dev):
     from neuroflow_amd import quant as Q
     layers = []
@@ -187,7 +201,9 @@ def main():
                 "unit": "TFLOP/s" if fmt == "fp8" else "TOPS",
                 "frac": round(tops / MFMA_PEAK_TOPS[fmt], 4), "traffic": None}
     N0, K0 = wl.layers[0].W.shape
-    roof.update({"kernel": "nfq::k_rows64" if K0 == 64 and N0 == 64 else "nfq::k_rows",
+    kernel = "nfq::k_rows64" if K0 == 64 and N0 == 64 else "nfq::k_rows"
+    roof["traffic"] = measured_traffic(kernel, args.workload)
+    roof.update({"kernel": kernel,
                  "kernel_avg_us": round(kernel_us, 3),
                  "bytes_per_launch": bytes_step // len(layers),
                  "ops_per_launch": ops_step // len(layers),

@@ -174,8 +174,10 @@ int nflow_fp8_e4m3_fake_quant(const float* in, float scale, float* out, int64_t 
 int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q,
                                  float* scale_A, void* stream);
 
-/* Fused FP8 layer: per-token FP8 quantise -> FP8 MFMA GEMM with fp32
- * accumulation -> (scale_W[n] * scale_A[m]) * acc + bias[n] -> activation.
+/* Fused FP8 layer: per-token FP8 quantise -> GEMM on the matrix cores with
+ * fp32 accumulation (E4M3 values are exact in bfloat16, so the product runs
+ * as bf16 MFMA on exact operands) -> (scale_W[n] * scale_A[m]) * acc +
+ * bias[n] -> activation.
  * No FP8 GEMM exists in the reference; its FP8 path is fake-quant followed by
  * the FP32 Linear loop (fp8_e4m3.h:312-334, fno.cpp:68-79). */
 int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M,

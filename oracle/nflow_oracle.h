@@ -7,9 +7,9 @@
  * (neuroflow_amd/, libnflow_quant.so) never links or calls it.
  *
  * Every function cites the reference file:line whose behaviour it restates
- * (paths relative to the NeuroFlow source tree).  Parity pins for each
- * function are listed in oracle/README.md and exercised by
- * tests/test_oracle_*.py.
+ * (paths relative to the NeuroFlow source tree).  Each function is pinned
+ * by tests/test_oracle_*.py against the reference's known-answer tests, its
+ * own build (oracle/_ref) or fixtures written by it, and closed forms.
  *
  * Build: plain C99, gcc -O2 -ffp-contract=off (no fast-math), so every
  * float expression rounds exactly as the reference's `-std=c++20` build does.

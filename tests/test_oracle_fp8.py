@@ -138,3 +138,93 @@ def test_fake_quant_matches_reference_build():
     for s in (1.0, 0.37, 0.0, 3e-3):
         assert np.array_equal(O.fp8_fake_quant(x, s).view(np.uint32),
                               O.ref_fp8_fake_quant(x, s).view(np.uint32))
+
+
+# ---- the FP8 layer: per-token / per-channel quantise, exact GEMM, composition ----
+
+def _fp8_rows(seed, M, K):
+    rng = np.random.default_rng(seed)
+    x = (2.0 * rng.standard_normal((M, K))).astype(np.float32)
+    x = np.where(rng.random((M, K)) < 0.01, 20.0 * x, x).astype(np.float32)
+    x[0] = 0.0
+    x[1] = 1e-41
+    x[2, :3] = [448.0, -3e5, 7.6 * 2.0 ** -9]
+    return x
+
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built on this host")
+def test_per_token_fp8_is_reference_fake_quant_per_row():
+    """Scale absmax/448 (1 for an all-zero row); decode(code) * scale equals the
+    reference's own fp8_e4m3_per_tensor_fake_quant of the row with that scale
+    (fp8_e4m3.h:312-334), element for element."""
+    x = _fp8_rows(11, 300, 64)
+    q, s = O.quantise_per_token_fp8(x)
+    am = np.abs(x).max(axis=1)
+    assert np.array_equal(_bits(s), _bits(np.where(am == 0, np.float32(1), am / np.float32(448))))
+    for m in range(x.shape[0]):
+        want = O.ref_fp8_fake_quant(x[m], float(s[m]))
+        assert np.array_equal(_bits(O.e4m3_decode(q[m]) * s[m]), _bits(want)), m
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built on this host")
+def test_fp8_weight_blob_is_reference_fake_quant_per_channel():
+    W = ((np.random.default_rng(12).random((96, 64)) - 0.5) * 0.25).astype(np.float32)
+    q, s = O.quantise_weight_fp8(W)
+    for n in range(W.shape[0]):
+        assert np.array_equal(_bits(O.e4m3_decode(q[n]) * s[n]),
+                              _bits(O.ref_fp8_fake_quant(W[n], float(s[n]))))
+
+
+def test_fp8_exact_gemm_is_the_float64_dot_product():
+    """E4M3 x E4M3 products are exact in float64 and a 64-term sum of them
+    spans fewer than 53 bits, so numpy's float64 product is the exact sum in
+    any summation order."""
+    rng = np.random.default_rng(13)
+    codes = np.array([b for b in range(256) if b not in (0x7F, 0xFF)], np.uint8)
+    qa = rng.choice(codes, (70, 64))
+    qw = rng.choice(codes, (40, 64))
+    want = O.e4m3_decode(qa).astype(np.float64) @ O.e4m3_decode(qw).astype(np.float64).T
+    assert np.array_equal(O.gemm_fp8_exact(qa, qw), want)
+    qa[5, 7] = 0x7F                                    # a NaN code poisons its row
+    got = O.gemm_fp8_exact(qa, qw)
+    assert np.isnan(got[5]).all() and not np.isnan(np.delete(got, 5, axis=0)).any()
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built on this host")
+def test_fp8_composed_layer_follows_reference_primitives():
+    """The composition: the reference build's fake-quant per row and per
+    channel, then the fp32 Linear loop of fno.cpp:68-79 (acc = bias, then
+    acc += a_k * w_k in k order), no activation: bit for bit."""
+    x = _fp8_rows(14, 48, 64)
+    W = ((np.random.default_rng(15).random((24, 64)) - 0.5) * 0.25).astype(np.float32)
+    b = ((np.random.default_rng(16).random(24) - 0.5) * 0.25).astype(np.float32)
+    got, sa, sw = O.layer_fp8_composed(x, W, b, O.ACT_NONE)
+    af = np.stack([O.ref_fp8_fake_quant(x[m], float(sa[m])) for m in range(x.shape[0])])
+    wf = np.stack([O.ref_fp8_fake_quant(W[n], float(sw[n])) for n in range(W.shape[0])])
+    acc = np.broadcast_to(b, got.shape).astype(np.float32)
+    for k in range(x.shape[1]):
+        acc = (acc + (af[:, k:k + 1] * wf[None, :, k])).astype(np.float32)
+    assert np.array_equal(_bits(got), _bits(acc))
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built on this host")
+def test_fp8_exact_layer_is_composition_without_accumulation_rounding():
+    """The exact-product layer differs from the reference composition only by
+    the composition's own fp32 accumulation: |diff| <= K 2^-24 sum|terms| + a
+    few ulp of the result."""
+    x = _fp8_rows(17, 64, 64)
+    W = ((np.random.default_rng(18).random((32, 64)) - 0.5) * 0.25).astype(np.float32)
+    b = ((np.random.default_rng(19).random(32) - 0.5) * 0.25).astype(np.float32)
+    composed, sa, sw = O.layer_fp8_composed(x, W, b, O.ACT_NONE)
+    qa, sa2 = O.quantise_per_token_fp8(x)
+    qw, sw2 = O.quantise_weight_fp8(W)
+    assert np.array_equal(_bits(sa), _bits(sa2)) and np.array_equal(_bits(sw), _bits(sw2))
+    exact = O.layer_fp8_exact(qa, sa2, qw, sw2, b, O.ACT_NONE).astype(np.float64)
+    terms = (np.abs(O.e4m3_decode(qa)) * sa2[:, None]).astype(np.float64) @ \
+        (np.abs(O.e4m3_decode(qw)) * sw2[:, None]).astype(np.float64).T
+    bound = 64 * 2.0 ** -24 * (terms + np.abs(b)) + 4 * 2.0 ** -24 * np.abs(exact) + 1e-30
+    assert np.all(np.abs(exact - composed) <= bound)
