@@ -1,0 +1,62 @@
+// gemm.hip -- launchers of the tiled INT8 MFMA GEMM (gemm_kernel.h).
+#include "gemm_kernel.h"
+#include "launch.h"
+
+namespace nfq {
+
+bool gemm_ok(const RowsArgs& a) {
+    // K <= 65536 keeps a 256-row tile's byte count inside the 32-bit buffer range.
+    return a.K % 64 == 0 && a.K >= 128 && a.K <= 65536 && a.N % 4 == 0 && a.kb_dot * 64 >= a.K &&
+           aligned(a.Aq, 16) && aligned(a.W, 16) && aligned(a.C, 16);
+}
+
+template <int TM, int TN, int OUT, int ACT>
+static void launch_gemm_t(const RowsArgs& a, hipStream_t st) {
+    auto kern = k_gemm<TM, TN, OUT, ACT>;
+    constexpr size_t lds = gemm_lds_bytes<TM, TN>();
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)attr;  // a failure surfaces as a launch error
+    using S = GemmShape<TM, TN>;
+    const int64_t blocks = ((a.M + S::BM - 1) / S::BM) * ((a.N + S::BN - 1) / S::BN);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, st, a);
+}
+
+// Tile shape: 128 x 256 for large M and N (two blocks per CU), else
+// 128 x 128 (more blocks for the small-M / narrow-N shapes).  Measured on
+// MI355X: 256 x 256 (one wave per SIMD) never beats 128 x 256, and 128 x 128
+// wins for M <= 4096 or N <= 768.
+static int gemm_shape(const RowsArgs& a) {
+    // NFLOW_GEMM_TILE=88|48|44 forces a shape (for tile sweeps).
+    if (const char* f = std::getenv("NFLOW_GEMM_TILE")) {
+        const int t = std::atoi(f);
+        if (t == 88 || t == 48 || t == 44) return t;
+    }
+    return (a.M >= 16384 && a.N >= 1024) ? 48 : 44;
+}
+
+template <int OUT, int ACT>
+static void launch_gemm_act(const RowsArgs& a, hipStream_t st) {
+    switch (gemm_shape(a)) {
+        case 88: launch_gemm_t<8, 8, OUT, ACT>(a, st); break;
+        case 48: launch_gemm_t<4, 8, OUT, ACT>(a, st); break;
+        default: launch_gemm_t<4, 4, OUT, ACT>(a, st); break;
+    }
+}
+
+template <int OUT>
+void launch_gemm(const RowsArgs& a, int act, hipStream_t st) {
+    if constexpr (OUT == OUT_RAW) {
+        launch_gemm_act<OUT, ACT_NONE>(a, st);
+    } else {
+        if (act == ACT_RELU) launch_gemm_act<OUT, ACT_RELU>(a, st);
+        else if (act == ACT_GELU_TANH) launch_gemm_act<OUT, ACT_GELU_TANH>(a, st);
+        else launch_gemm_act<OUT, ACT_NONE>(a, st);
+    }
+}
+
+template void launch_gemm<OUT_EPI>(const RowsArgs&, int, hipStream_t);
+template void launch_gemm<OUT_RAW>(const RowsArgs&, int, hipStream_t);
+
+}  // namespace nfq

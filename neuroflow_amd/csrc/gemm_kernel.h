@@ -1,0 +1,266 @@
+// gemm_kernel.h -- tiled MFMA GEMM on INT8 codes with the fused epilogue,
+// for the wide shapes (K a multiple of 64, K >= 128): C[m][n] =
+// epilogue(sum_k A_q[m][k] * W_q[n][k]).
+//
+// A block of 4 waves (2 x 2) computes a BM x BN tile, BM = 32 TM, BN = 32 TN;
+// wave (wm, wn) owns rows 16 TM wm .. and columns 16 TN wn .. as TM x TN
+// MFMA tiles of v_mfma_i32_16x16x64_i8 (W as the A operand, so lane (r, g)
+// of a tile holds row r, columns 4g .. 4g + 3).  K advances 64 per step
+// through two LDS stages: each thread loads 16-byte chunks of the A and W
+// tiles into registers one step ahead, adds their byte sums to its row /
+// column partial sums (needed by the zero-point terms), and stores them into
+// the stage not being read.  Rows of both LDS tiles are 64 bytes with the
+// 16-byte group g of row `row` stored at slot g ^ ((row >> 1) & 3): measured
+// on gfx950, this reads 16-row x 16-byte operand fragments at the rate of a
+// contiguous ds_read_b128 (a 64- or 80-byte stride without it is 2-4 way
+// bank conflicted).
+#pragma once
+
+#include "common.h"
+#include "rows_kernel.h"
+
+namespace nfq {
+
+constexpr int GEMM_LDS_ROW = 64;  // bytes per K row in LDS
+
+// Byte offset of 16-byte group g of row `row` within a stage tile.
+__device__ __forceinline__ int gemm_lds_off(int row, int g) {
+    return row * GEMM_LDS_ROW + 16 * (g ^ ((row >> 1) & 3));
+}
+
+template <int TM, int TN>
+struct GemmShape {
+    static constexpr int BM = 32 * TM;
+    static constexpr int BN = 32 * TN;
+    static constexpr int A_CHUNKS = BM * 4 / 256;  // 16-byte chunks per thread per K step
+    static constexpr int W_CHUNKS = BN * 4 / 256;
+    static constexpr int STAGE = (BM + BN) * GEMM_LDS_ROW;
+};
+
+// Buffer resource over rows [row0, row0 + rows) of a row-major array with
+// `row_bytes` bytes per row and `total_rows` rows (reads past the end are 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t row0,
+                                                            int64_t total_rows, int rows,
+                                                            int64_t row_bytes) {
+    int64_t left = total_rows - row0;
+    left = left < 0 ? 0 : (left > rows ? rows : left);
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(base)) + row0 * row_bytes, 0,
+        static_cast<int>(left * row_bytes), 0x00020000);
+}
+
+// Waves per SIMD the tile shape is built for: the 256 x 256 tile holds its
+// accumulators in all 256 AGPRs (one wave per SIMD); smaller tiles fit two.
+constexpr int gemm_min_waves(int TM, int TN) { return TM * TN >= 64 ? 1 : 2; }
+
+template <int TM, int TN, int OUT, int ACT>
+__global__ __launch_bounds__(256, gemm_min_waves(TM, TN)) void k_gemm(RowsArgs a) {
+    using S = GemmShape<TM, TN>;
+    constexpr int BM = S::BM, BN = S::BN;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    // Epilogue tables after the two stages.
+    int32_t* lds_sa = reinterpret_cast<int32_t*>(lds + 2 * S::STAGE);      // BM row code sums
+    int32_t* lds_sw = lds_sa + BM;                                          // BN weight sums
+    IntEpi* lds_e = reinterpret_cast<IntEpi*>(lds_sw + BN);                 // BN constants
+    float* lds_scw = reinterpret_cast<float*>(lds_e + BN);                  // BN scale_W
+    float* lds_b = lds_scw + BN;                                            // BN bias
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const int r = lane & 15, g = lane >> 4;
+    const int K = a.K;
+    const int64_t M = a.M;
+    const int N = a.N;
+    // Block order: consecutive blocks share an A row tile (N tiles inner).
+    const int n_tiles = (N + BN - 1) / BN;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x / n_tiles) * BM;
+    const int n0 = static_cast<int>(blockIdx.x % n_tiles) * BN;
+
+    const auto rs_a = rows_rsrc(a.Aq, m0, M, BM, K);
+    const auto rs_w = rows_rsrc(a.W, n0, N, BN, K);
+
+    // Chunk c of this thread: tile row (tid >> 2) + 64 c, 16-byte column tid & 3.
+    const int crow = tid >> 2, ccol = tid & 3;
+    v4u ra[S::A_CHUNKS], rw[S::W_CHUNKS];
+    int32_t psa[S::A_CHUNKS], psw[S::W_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < S::A_CHUNKS; ++c) psa[c] = 0;
+#pragma unroll
+    for (int c = 0; c < S::W_CHUNKS; ++c) psw[c] = 0;
+
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int c = 0; c < S::A_CHUNKS; ++c)
+            ra[c] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, (crow + 64 * c) * K + k0 + 16 * ccol, 0, 0);
+#pragma unroll
+        for (int c = 0; c < S::W_CHUNKS; ++c)
+            rw[c] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, (crow + 64 * c) * K + k0 + 16 * ccol, 0, 0);
+    };
+    auto sstore = [&](uint8_t* st) {
+#pragma unroll
+        for (int c = 0; c < S::A_CHUNKS; ++c) {
+            *reinterpret_cast<v4u*>(st + gemm_lds_off(crow + 64 * c, ccol)) = ra[c];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) psa[c] = sum_bytes_i8(ra[c][q], psa[c]);
+        }
+#pragma unroll
+        for (int c = 0; c < S::W_CHUNKS; ++c) {
+            *reinterpret_cast<v4u*>(st + BM * GEMM_LDS_ROW + gemm_lds_off(crow + 64 * c, ccol)) = rw[c];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) psw[c] = sum_bytes_i8(rw[c][q], psw[c]);
+        }
+    };
+
+    v4i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const int ksteps = K / 64;
+    gload(0);
+    sstore(lds);
+    __syncthreads();
+    for (int ks = 0; ks < ksteps; ++ks) {
+        const uint8_t* cur = lds + (ks & 1) * S::STAGE;
+        const bool more = ks + 1 < ksteps;
+        if (more) gload((ks + 1) * 64);
+        v4i xf[TM], wf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            xf[i] = *reinterpret_cast<const v4i*>(cur + gemm_lds_off(16 * TM * wm + 16 * i + r, g));
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            wf[j] = *reinterpret_cast<const v4i*>(cur + BM * GEMM_LDS_ROW + gemm_lds_off(16 * TN * wn + 16 * j + r, g));
+        // All fragment reads before the first MFMA: one LDS round trip per
+        // K step instead of one per row tile.
+        __builtin_amdgcn_sched_group_barrier(0x0100, TM + TN, 0);  // DS reads
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[j], xf[i], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x0008, TM * TN, 0);  // MFMA
+        if (more) sstore(lds + ((ks + 1) & 1) * S::STAGE);
+        __syncthreads();
+    }
+
+    // Row / column byte sums: reduce the 4 threads (ccol) of each tile row.
+#pragma unroll
+    for (int c = 0; c < S::A_CHUNKS; ++c) {
+        int32_t v = psa[c];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (ccol == 0) lds_sa[crow + 64 * c] = v;
+    }
+#pragma unroll
+    for (int c = 0; c < S::W_CHUNKS; ++c) {
+        int32_t v = psw[c];
+        v += __shfl_xor(v, 1);
+        v += __shfl_xor(v, 2);
+        if (ccol == 0) lds_sw[crow + 64 * c] = v;
+    }
+    __syncthreads();
+    bool trivial = true;  // every column's integer constants are zero
+    if constexpr (OUT == OUT_EPI) {
+        bool nonzero = false;
+        for (int c = tid; c < BN; c += 256) {
+            const int n = n0 + c;
+            IntEpi e{0, 0, 0};
+            float sw = 0.0f, b = 0.0f;
+            if (n < N) {
+                const int32_t zpw = a.zpW ? a.zpW[n] : 0;
+                const int32_t swg = a.sumW ? a.sumW[n] : 0;
+                // K is a multiple of 64, so the dot covers every k and Wd = Sfull.
+                e = int_epi_consts(a.formula, K, a.zp_A, zpw, swg, a.sumW != nullptr, lds_sw[c], lds_sw[c]);
+                sw = a.sW[n];
+                b = a.bias ? a.bias[n] : 0.0f;
+            }
+            nonzero |= (e.c0 != 0) | (e.c1 != 0) | (e.c2 != 0);
+            lds_e[c] = e;
+            lds_scw[c] = sw;
+            lds_b[c] = b;
+        }
+        trivial = __syncthreads_count(nonzero) == 0;
+    }
+
+    // Epilogue, one 16-row strip (tile row i) at a time.  Lane (r, g) of
+    // tile (i, j) holds row 16 TM wm + 16 i + r, columns 16 TN wn + 16 j +
+    // 4 g .. + 3; the wave writes its strip (16 rows x 16 TN columns) into its
+    // own LDS area in the stage buffers (free after the last K step's
+    // barrier), then reads it back row-contiguously, so each store
+    // instruction writes 64 / (4 TN) rows of 64 TN contiguous bytes.
+    constexpr int SW = 16 * TN + 4;                 // strip row stride (32-bit words)
+    constexpr int CHUNKS = 4 * TN;                  // 16-byte chunks per strip row
+    constexpr int ROWS_PER_INST = 64 / CHUNKS;
+    static_assert(4 * 16 * SW * 4 <= 2 * GemmShape<TM, TN>::STAGE, "strip areas fit the stages");
+    uint32_t* strip = reinterpret_cast<uint32_t*>(lds) + wid * 16 * SW;
+    float srow[TM];
+    int32_t sa[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int lrow = 16 * TM * wm + 16 * i + r;
+        const int64_t m = m0 + lrow;
+        srow[i] = 1.0f;
+        sa[i] = 0;
+        if constexpr (OUT == OUT_EPI) {
+            srow[i] = m < M ? (a.scale_in ? a.scale_in[m] : a.scale_A) : 0.0f;
+            sa[i] = lds_sa[lrow];
+        }
+    }
+    const int ncol0 = n0 + 16 * TN * wn;            // first column of the wave's tile
+    const int rd_row = lane / CHUNKS, rd_chunk = lane % CHUNKS;
+    const bool col_ok = ncol0 + 4 * rd_chunk < N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int lcol = 16 * TN * wn + 16 * j + 4 * g;
+            v4u bits;
+            if constexpr (OUT == OUT_RAW) {
+                bits = __builtin_bit_cast(v4u, acc[i][j]);
+            } else {
+                const v4f swv = *reinterpret_cast<const v4f*>(lds_scw + lcol);
+                const v4f bv = *reinterpret_cast<const v4f*>(lds_b + lcol);
+                v4f y;
+                if (trivial) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        y[v] = activate<ACT>(dequant_bias(swv[v], srow[i], static_cast<float>(acc[i][j][v]), bv[v]));
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float t = int_epi_value(lds_e[lcol + v], acc[i][j][v], sa[i]);
+                        y[v] = activate<ACT>(dequant_bias(swv[v], srow[i], t, bv[v]));
+                    }
+                }
+                bits = __builtin_bit_cast(v4u, y);
+            }
+            *reinterpret_cast<v4u*>(strip + r * SW + 16 * j + 4 * g) = bits;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int q = 0; q < 16 / ROWS_PER_INST; ++q) {
+            const int srow_i = q * ROWS_PER_INST + rd_row;
+            const v4u v = *reinterpret_cast<const v4u*>(strip + srow_i * SW + 4 * rd_chunk);
+            const int64_t m = m0 + 16 * TM * wm + 16 * i + srow_i;
+            if (m < M && col_ok)
+                *reinterpret_cast<v4u*>(static_cast<uint32_t*>(a.C) + m * N + ncol0 + 4 * rd_chunk) = v;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+template <int TM, int TN>
+constexpr size_t gemm_lds_bytes() {
+    using S = GemmShape<TM, TN>;
+    return 2 * S::STAGE + (S::BM + S::BN) * sizeof(int32_t) + S::BN * (sizeof(IntEpi) + 2 * sizeof(float));
+}
+
+}  // namespace nfq

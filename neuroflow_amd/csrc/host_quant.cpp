@@ -11,7 +11,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/nflow_quant.h"
+#include "nflow_quant.h"
 #include "status.h"
 
 namespace nfq {

@@ -10,7 +10,7 @@
 #include <cstdlib>
 #include <mutex>
 
-#include "../../include/nflow_quant.h"
+#include "nflow_quant.h"
 #include "rows_kernel.h"
 
 namespace nfq {
@@ -78,5 +78,10 @@ void launch_rows(const RowsArgs& a, int act, hipStream_t st);
 bool rows64_ok(const RowsArgs& a);
 template <bool FP8>
 void launch_rows64(const RowsArgs& a, int act, hipStream_t st);
+
+// The tiled MFMA GEMM on INT8 codes for K a multiple of 64, K >= 128 (gemm.hip).
+bool gemm_ok(const RowsArgs& a);
+template <int OUT>
+void launch_gemm(const RowsArgs& a, int act, hipStream_t st);
 
 }  // namespace nfq

@@ -15,7 +15,7 @@
 #include <mutex>
 #include <string>
 
-#include "../../include/nflow_quant.h"
+#include "nflow_quant.h"
 #include "common.h"
 #include "launch.h"
 #include "rows_kernel.h"
@@ -167,6 +167,56 @@ __global__ __launch_bounds__(256) void k_generic(RowsArgs a, int act) {
     }
 }
 
+// The same for rows of K = 256 KV floats: the row stays in registers (KV
+// float4 per lane), so HBM is read once, in 1 KB wave instructions, and the
+// codes leave as one dword per lane per float4.
+template <bool FP8, int KV>
+__global__ __launch_bounds__(256) void k_quantise_rows(const float* __restrict__ A, int64_t M,
+                                                       uint8_t* __restrict__ Aq,
+                                                       float* __restrict__ scale,
+                                                       int32_t* __restrict__ sum_a) {
+    constexpr int K = 256 * KV;
+    const int lane = threadIdx.x & 63;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); m < M; m += nw) {
+        const v4f* x4 = reinterpret_cast<const v4f*>(A + m * K);
+        v4f x[KV];
+#pragma unroll
+        for (int i = 0; i < KV; ++i) x[i] = x4[lane + 64 * i];
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KV; ++i)
+            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(x[i][0]), fabsf(x[i][1]))), fmaxf(fabsf(x[i][2]), fabsf(x[i][3])));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float s = (mx == 0.0f) ? 1.0f : mx / (FP8 ? 448.0f : 127.0f);
+        uint32_t* q4 = reinterpret_cast<uint32_t*>(Aq + m * K);
+        int32_t sa = 0;
+        if constexpr (FP8) {
+            const float inv = (s == 0.0f) ? 1.0f : 1.0f / s;
+#pragma unroll
+            for (int i = 0; i < KV; ++i)
+                q4[lane + 64 * i] = fp8_quant(x[i][0], inv) | (fp8_quant(x[i][1], inv) << 8) |
+                                    (fp8_quant(x[i][2], inv) << 16) | (fp8_quant(x[i][3], inv) << 24);
+        } else {
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int i = 0; i < KV; ++i) {
+                const uint32_t w = pack4(quant_i8_token(x[i][0], s, inv), quant_i8_token(x[i][1], s, inv),
+                                         quant_i8_token(x[i][2], s, inv), quant_i8_token(x[i][3], s, inv));
+                q4[lane + 64 * i] = w;
+                sa = sum_bytes_i8(w, sa);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sa += __shfl_xor(sa, o);
+        }
+        if (lane == 0) {
+            scale[m] = s;
+            if (sum_a) sum_a[m] = sa;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Launch helpers
 // ---------------------------------------------------------------------------
@@ -175,6 +225,26 @@ template <bool FP8, int OUT>
 static void launch_generic(const RowsArgs& a, int act, hipStream_t st) {
     const unsigned grid = grid_for(a.M * a.N, 256, 16);
     hipLaunchKernelGGL((k_generic<FP8, OUT>), dim3(grid), dim3(256), 0, st, a, act);
+}
+
+// Per-token quantise of (M, K) rows: the register-resident kernel for
+// K = 256, 512, 1024, 2048, 4096 (16-byte aligned rows), else one wave per
+// row with a loop over K.
+template <bool FP8>
+static void launch_quantise_token(const float* A, int64_t M, int K, uint8_t* Aq, float* scale,
+                                  int32_t* sum_a, hipStream_t st) {
+    const dim3 grid(grid_for(M, 4, 16)), block(256);
+    if (aligned(A, 16) && aligned(Aq, 4)) {
+        switch (K) {
+            case 256: hipLaunchKernelGGL((k_quantise_rows<FP8, 1>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            case 512: hipLaunchKernelGGL((k_quantise_rows<FP8, 2>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            case 1024: hipLaunchKernelGGL((k_quantise_rows<FP8, 4>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            case 2048: hipLaunchKernelGGL((k_quantise_rows<FP8, 8>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            case 4096: hipLaunchKernelGGL((k_quantise_rows<FP8, 16>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            default: break;
+        }
+    }
+    hipLaunchKernelGGL((k_quantise_token<FP8>), grid, block, 0, st, A, M, K, Aq, scale, sum_a);
 }
 
 static int check_launch(const char* what) {
@@ -233,6 +303,10 @@ static int int8_fixed_path(const nflow_int8_linear_params* p, int64_t rows, cons
     launch_generic<false, OUT_EPI>(a, ACT_NONE, st);
     return check_launch(what);
 }
+
+// The tiled GEMM serves INT8 code input with K a multiple of 64, K >= 128
+// (NFLOW_NO_GEMM=1 selects the row-tile kernel instead, for A/B timing).
+static bool use_gemm(const RowsArgs& a) { return gemm_ok(a) && !getenv_flag("NFLOW_NO_GEMM"); }
 
 static int check_params(const nflow_int8_linear_params* p, const char* what) {
     if (!p || !p->W_int8 || !p->scale_W || !p->zp_W)
@@ -310,8 +384,7 @@ int nflow_int8_quantise_per_token(const float* A, int64_t M, int K, int8_t* A_q,
     if (!A || !A_q || !scale_A) return set_error(NFLOW_INVALID_ARG, "quantise_per_token: null pointer");
     if (K <= 0) return set_error(NFLOW_INVALID_ARG, "quantise_per_token: K <= 0");
     if (M <= 0) return NFLOW_OK;
-    hipLaunchKernelGGL((k_quantise_token<false>), dim3(grid_for(M, 4, 16)), dim3(256), 0,
-                       as_stream(stream), A, M, K, reinterpret_cast<uint8_t*>(A_q), scale_A, sum_a);
+    launch_quantise_token<false>(A, M, K, reinterpret_cast<uint8_t*>(A_q), scale_A, sum_a, as_stream(stream));
     return check_launch("quantise_per_token");
 }
 
@@ -346,7 +419,11 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
         launch_rows64<false>(a, activation, st);
         return check_launch("linear_forward_per_token");
     }
-    if (rows_ok(a, IN_F32_TOKEN)) {
+    // Wide K: quantise into a workspace, then the tiled GEMM (below).
+    RowsArgs g = a;
+    g.Aq = nullptr;  // the codes go to the workspace, which is 256-byte aligned
+    const bool wide = use_gemm(g);
+    if (!wide && rows_ok(a, IN_F32_TOKEN)) {
         launch_rows<false, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
         return check_launch("linear_forward_per_token");
     }
@@ -356,12 +433,12 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
     if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_per_token: workspace allocation failed");
     uint8_t* q = static_cast<uint8_t*>(ws.p);
     float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
-    hipLaunchKernelGGL((k_quantise_token<false>), dim3(grid_for(M, 4, 16)), dim3(256), 0, st, A, M,
-                       a.K, q, sc, static_cast<int32_t*>(nullptr));
+    launch_quantise_token<false>(A, M, a.K, q, sc, static_cast<int32_t*>(nullptr), st);
     if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
     a.Aq = q;
     a.scale_in = sc;
-    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, st);
+    if (wide) launch_gemm<OUT_EPI>(a, activation, st);
+    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, st);
     else launch_generic<false, OUT_EPI>(a, activation, st);
     return check_launch("linear_forward_per_token");
 }
@@ -380,7 +457,8 @@ int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, 
     a.W = reinterpret_cast<const uint8_t*>(W_q);
     a.kb_dot = (K + 63) / 64;
     a.C = C;
-    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    if (use_gemm(a)) launch_gemm<OUT_RAW>(a, ACT_NONE, as_stream(stream));
+    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_RAW>(a, ACT_NONE, as_stream(stream));
     else launch_generic<false, OUT_RAW>(a, ACT_NONE, as_stream(stream));
     return check_launch("gemm_i32");
 }
@@ -411,7 +489,8 @@ int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64
     a.formula = formula_row(a.K);
     a.kb_dot = kb_dot_for(a.formula, a.K);
     a.C = C;
-    if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
+    if (use_gemm(a)) launch_gemm<OUT_EPI>(a, activation, as_stream(stream));
+    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
     else launch_generic<false, OUT_EPI>(a, activation, as_stream(stream));
     return check_launch("linear_forward_quantised");
 }
@@ -449,8 +528,7 @@ int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q,
     if (!A || !A_q || !scale_A) return set_error(NFLOW_INVALID_ARG, "fp8_quantise_per_token: null pointer");
     if (K <= 0) return set_error(NFLOW_INVALID_ARG, "fp8_quantise_per_token: K <= 0");
     if (M <= 0) return NFLOW_OK;
-    hipLaunchKernelGGL((k_quantise_token<true>), dim3(grid_for(M, 4, 16)), dim3(256), 0,
-                       as_stream(stream), A, M, K, A_q, scale_A, static_cast<int32_t*>(nullptr));
+    launch_quantise_token<true>(A, M, K, A_q, scale_A, static_cast<int32_t*>(nullptr), as_stream(stream));
     return check_launch("fp8_quantise_per_token");
 }
 
@@ -494,8 +572,7 @@ int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t
     if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "fp8_linear_forward_per_token: workspace allocation failed");
     uint8_t* q = static_cast<uint8_t*>(ws.p);
     float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
-    hipLaunchKernelGGL((k_quantise_token<true>), dim3(grid_for(M, 4, 16)), dim3(256), 0, st, A, M,
-                       a.K, q, sc, static_cast<int32_t*>(nullptr));
+    launch_quantise_token<true>(A, M, a.K, q, sc, static_cast<int32_t*>(nullptr), st);
     if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
     a.Aq = q;
     a.scale_in = sc;

@@ -49,7 +49,7 @@ def test_decode_and_fake_quant(gpu):
     assert np.array_equal(Q.fp8_e4m3_to_bits(x[:100]), O.e4m3_encode(x[:100]))
 
 
-@pytest.mark.parametrize("M,K", [(1, 64), (999, 64), (100, 256), (10, 100)])
+@pytest.mark.parametrize("M,K", [(1, 64), (999, 64), (100, 256), (10, 100), (70, 1024), (5, 4096)])
 def test_quantise_per_token_fp8(gpu, M, K):
     x = 2.0 * WL.normal(31, (M, K))
     x[0, :4] = [1e-4, -1e-5, 448.0, 0.0]
@@ -131,3 +131,21 @@ def test_fp8_layer_k64_special_rows(gpu, act):
     assert np.array_equal(np.isnan(out), np.isnan(exact))
     fin = ~np.isnan(exact)
     np.testing.assert_allclose(out[fin], exact[fin], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("K", [256, 1024])
+def test_quantise_per_token_fp8_special_rows(gpu, K):
+    """The register-resident quantise (K = 256 KV) on zero, NaN, signalling
+    NaN, infinite, subnormal and saturating rows: scales and bytes bit-exact."""
+    x = (2.0 * WL.normal(41, (9, K))).astype(np.float32)
+    x[1] = 0.0
+    x[2] = np.nan
+    x[3, 5] = np.nan
+    x.view(np.uint32)[4, 7] = 0x7F800001
+    x[5, 1] = -np.inf
+    x[6] = 1e-41
+    x[7, :3] = [3e38, 470.0, -7.6 * 2.0 ** -9]
+    q, s = Q.fp8_quantise_per_token(_cu(x))
+    q_ref, s_ref = O.quantise_per_token_fp8(x)
+    assert np.array_equal(_host(s).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(_host(q), q_ref)

@@ -67,6 +67,27 @@ def test_quantise_per_token_ties_and_specials(gpu):
     assert np.array_equal(_host(q), q_ref)
 
 
+@pytest.mark.parametrize("K", [256, 1024])
+def test_quantise_per_token_special_rows_wide(gpu, K):
+    """The register-resident quantise (K = 256 KV) on exact ties, zero, NaN,
+    signalling NaN, infinite and subnormal rows: codes, scales and sums."""
+    A = (WL.normal(42, (9, K)) * 3.0).astype(np.float32)
+    A[0, 0] = 127.0
+    A[0, 1:] = (np.arange(1, K, dtype=np.float32) % 200 - 100.0) * 0.5   # k + 0.5 ties
+    A[1] = 0.0
+    A[2] = np.nan
+    A[3, 9] = np.nan
+    A.view(np.uint32)[4, 3] = 0x7F800001
+    A[5, 2] = np.inf
+    A[6] = 1e-40
+    A[7, :] *= 3e-37 / np.abs(A[7]).max()
+    q, s, sa = Q.quantise_per_token(_cu(A))
+    q_ref, s_ref, sa_ref = O.quantise_per_token_i8(A)
+    assert _bits_equal(_host(s), s_ref)
+    assert np.array_equal(_host(q), q_ref)
+    assert np.array_equal(_host(sa), sa_ref)
+
+
 @pytest.mark.parametrize("scale,zp", [(0.05, 0), (0.05, 3), (0.03, -7), (0.0, 0), (1.0, 100)])
 def test_quantise_activation_bit_exact(gpu, scale, zp):
     A = WL.normal(12, (300, 96)) * 4.0
@@ -211,3 +232,58 @@ def test_fused_k64_layer_asymmetric_weights(gpu):
         out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
         ref, _ = O.layer_per_token_i8(A, q, s, zps, b, sumW, 0)
         assert _bits_equal(out, ref)
+
+
+# ---- the tiled GEMM (K a multiple of 64, K >= 128): every tile shape ----------
+
+# (M, N, K) choosing the 256x256, 128x256 and 128x128 block tiles on 256 CUs.
+GEMM_SHAPES = [(16384, 1024, 256), (8192, 1024, 128), (2000, 200, 192), (1, 64, 128)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_i32_tile_shapes(gpu, M, N, K):
+    """int32 accumulators of every tile shape, bit-exact; the float64 product
+    is exact here (|sum| <= K * 128^2 < 2^24)."""
+    A = WL.uniform(30, (M, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
+    W = WL.uniform(31, (N, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
+    A[-1, :] = -128
+    W[-1, :] = -128
+    got = _host(Q.gemm_i32(_cu(A), _cu(W)))
+    want = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:3])
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_gemm_per_token_layer_tile_shapes(gpu, M, N, K, act):
+    """The per-token layer through quantise + tiled GEMM, on sampled rows
+    (each output row depends only on its input row)."""
+    A = WL.normal(32, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 33)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw))
+    out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
+    out, sa = _host(out), _host(sa)
+    rows = np.unique(np.concatenate([np.arange(0, M, 97), [M - 1]]))
+    ref, sa_ref = O.layer_per_token_i8(A[rows], q, s, zps, b, sw, {"none": 0, "gelu": 2}[act])
+    assert _bits_equal(sa[rows], sa_ref)
+    if act == "gelu":
+        np.testing.assert_allclose(out[rows], ref, rtol=RTOL, atol=ATOL)
+    else:
+        assert _bits_equal(out[rows], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 256, 256), (70, 512, 1024), (9000, 1024, 128),
+                                   (16384, 1024, 256), (8192, 1024, 128)])
+@pytest.mark.parametrize("with_sum", [False, True])
+def test_gemm_layer_asymmetric_weights(gpu, M, N, K, with_sum):
+    """Zero points through the tiled GEMM: the row code sums and weight sums it
+    accumulates feed LinearForward's formula (int8_gemm.cpp:386-393, 461-467)."""
+    A = WL.normal(34, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 35, zp=True)
+    sumW = sw if with_sum else None
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b),
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
+    rows = np.unique(np.concatenate([np.arange(0, M, 13), [M - 1]]))
+    ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, 0)
+    assert _bits_equal(out[rows], ref)
