@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define NFLOW_QUANT_ABI_VERSION 1
+#define NFLOW_QUANT_ABI_VERSION 2
 
 /* nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37. */
 enum nflow_status_code {
@@ -79,6 +79,12 @@ typedef struct nflow_fp8_linear_params {
     int in_features;
     int out_features;
 } nflow_fp8_linear_params;
+
+/* Weight format of a layer handle. */
+enum nflow_format {
+    NFLOW_FORMAT_INT8 = 0,       /* per-channel symmetric int8, per-token int8 activations */
+    NFLOW_FORMAT_FP8_E4M3 = 1    /* per-channel E4M3, per-token E4M3 activations */
+};
 
 /* ---- library ------------------------------------------------------------ */
 
@@ -213,6 +219,40 @@ int nflow_host_per_channel_scales(const float* W, int out_features, int in_featu
  * zero row), W_q = fp32_to_e4m3_bits(clamp(W * (1/scales[c]), -448, 448)). */
 int nflow_host_fp8_quantise_weight(const float* W, int out_features, int in_features,
                                    uint8_t* W_q, float* scales);
+
+/* ---- device-resident layers ---------------------------------------------
+ * The Int8GemmLayer cache of fno::FNO1d::EnableInt8Gemm (cpp/src/fno.cpp:
+ * 325-406, cpp/include/neuroflow/fno.h:66-87) as an opaque handle whose weight
+ * blob lives in device memory: built and uploaded once, then used by every
+ * forward call.  Creation allocates on the current device (hipMalloc) and is
+ * not stream-ordered; forward is.  A handle must not be destroyed while work
+ * that uses it is pending. */
+typedef struct nflow_layer nflow_layer;
+
+/* From host fp32 weights W (out_features, in_features) and an optional host
+ * bias: INT8 builds scales = absmax/127 per channel and codes by
+ * QuantiseWeight2D with zero points 0 (plus sum_W_per_row); FP8 builds
+ * scales = absmax/448 and E4M3 codes. */
+int nflow_layer_create(const float* W, const float* bias, int out_features, int in_features,
+                       int format, nflow_layer** layer);
+
+/* From an existing INT8 blob (host pointers): codes, per-channel scales and
+ * zero points, optional bias and sum_W_per_row -- the per-channel qparams a
+ * NIRQ file carries (cpp/include/neuroflow/ir_loader.h:556-650). */
+int nflow_layer_create_int8(const int8_t* W_q, const float* scale_W, const int32_t* zp_W,
+                            const float* bias, const int32_t* sum_W_per_row, int out_features,
+                            int in_features, nflow_layer** layer);
+
+/* The fused per-token layer on device buffers x (M, in_features) and
+ * y (M, out_features): nflow_int8_linear_forward_per_token or
+ * nflow_fp8_linear_forward_per_token with the handle's blob. */
+int nflow_layer_forward(const nflow_layer* layer, int64_t M, const float* x, float* y,
+                        float* scale_A_out, int activation, void* stream);
+
+int nflow_layer_shape(const nflow_layer* layer, int* out_features, int* in_features, int* format);
+
+/* Frees the handle and its device memory (NULL is allowed). */
+int nflow_layer_destroy(nflow_layer* layer);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ STATUS_NAMES = {0: "Ok", 1: "InvalidArg", 2: "FileNotFound", 3: "ParseError",
                 4: "ShapeMismatch", 5: "UnsupportedOp", 99: "Internal"}
 
 ACT_NONE, ACT_RELU, ACT_GELU_TANH = 0, 1, 2
+FORMAT_INT8, FORMAT_FP8_E4M3 = 0, 1
 
 
 class Int8LinearParamsC(C.Structure):
@@ -79,6 +80,11 @@ SIGNATURES = {
     "nflow_host_quantise_weight_2d": [_vp, _i32, _i32, _vp, _vp, _vp, _vp],
     "nflow_host_per_channel_scales": [_vp, _i32, _i32, _f32, _vp],
     "nflow_host_fp8_quantise_weight": [_vp, _i32, _i32, _vp, _vp],
+    "nflow_layer_create": [_vp, _vp, _i32, _i32, _i32, C.POINTER(_vp)],
+    "nflow_layer_create_int8": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(_vp)],
+    "nflow_layer_forward": [_vp, _i64, _vp, _vp, _vp, _i32, _vp],
+    "nflow_layer_shape": [_vp, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)],
+    "nflow_layer_destroy": [_vp],
 }
 _RESTYPES = {"nflow_last_error": C.c_char_p}
 

@@ -421,3 +421,73 @@ class Fp8Linear:
 
         run.params = ps
         return run
+
+
+# ---- device-resident layer handles (nflow_layer) -----------------------------
+
+_FORMATS = {"int8": _lib.FORMAT_INT8, "fp8": _lib.FORMAT_FP8_E4M3}
+
+
+class Layer:
+    """A `nflow_layer` handle: the library quantises the weights, uploads the
+    blob once to the current device and owns it (the Int8GemmLayer cache of
+    EnableInt8Gemm, fno.cpp:325-406); calls run the fused per-token kernel.
+
+    Layer(W, bias, fmt="int8"|"fp8") builds from fp32 weights;
+    Layer.from_int8_blob(W_q, scale_W, zp_W, bias, sum_W) from an existing
+    INT8 blob (the per-channel qparams of an IR file)."""
+
+    def __init__(self, W: Optional[np.ndarray] = None, bias: Optional[np.ndarray] = None,
+                 fmt: str = "int8", _handle=None):
+        self._h = C.c_void_p()
+        if _handle is not None:
+            self._h = _handle
+        else:
+            if fmt not in _FORMATS:
+                raise ValueError(f"unknown format {fmt!r}")
+            W = np.ascontiguousarray(W, np.float32)
+            b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+            check(_lib.lib().nflow_layer_create(_np_ptr(W), None if b is None else _np_ptr(b),
+                                                W.shape[0], W.shape[1], _FORMATS[fmt],
+                                                C.byref(self._h)), "layer_create")
+        n, k, f = C.c_int(), C.c_int(), C.c_int()
+        check(_lib.lib().nflow_layer_shape(self._h, C.byref(n), C.byref(k), C.byref(f)), "layer_shape")
+        self.out_features, self.in_features = n.value, k.value
+        self.fmt = "int8" if f.value == _lib.FORMAT_INT8 else "fp8"
+
+    @classmethod
+    def from_int8_blob(cls, W_q, scale_W, zp_W, bias=None, sum_W=None) -> "Layer":
+        W_q = np.ascontiguousarray(W_q, np.int8)
+        arrs = [np.ascontiguousarray(scale_W, np.float32), np.ascontiguousarray(zp_W, np.int32),
+                None if bias is None else np.ascontiguousarray(bias, np.float32),
+                None if sum_W is None else np.ascontiguousarray(sum_W, np.int32)]
+        h = C.c_void_p()
+        check(_lib.lib().nflow_layer_create_int8(
+            _np_ptr(W_q), *[None if a is None else _np_ptr(a) for a in arrs],
+            W_q.shape[0], W_q.shape[1], C.byref(h)), "layer_create_int8")
+        return cls(_handle=h)
+
+    def __call__(self, x: torch.Tensor, activation="gelu", out: Optional[torch.Tensor] = None,
+                 return_scales: bool = False):
+        _dev(x, torch.float32, "x")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"x has {x.shape[-1]} features, the layer takes {self.in_features}")
+        M = x.numel() // self.in_features
+        if out is None:
+            out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.float32, device=x.device)
+        s = torch.empty(M, dtype=torch.float32, device=x.device) if return_scales else None
+        check(_lib.lib().nflow_layer_forward(self._h, M, x.data_ptr(), out.data_ptr(),
+                                             None if s is None else s.data_ptr(), _act(activation),
+                                             _stream()), "layer_forward")
+        return (out, s) if return_scales else out
+
+    def close(self) -> None:
+        if self._h:
+            _lib.lib().nflow_layer_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

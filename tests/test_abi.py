@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_values():
-    assert _lib.lib().nflow_quant_abi_version() == 1
+    assert _lib.lib().nflow_quant_abi_version() == 2
     text = HEADER.read_text()
     # nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37
     for name, val in [("NFLOW_OK", 0), ("NFLOW_INVALID_ARG", 1), ("NFLOW_FILE_NOT_FOUND", 2),
@@ -70,3 +70,25 @@ def test_host_entry_points_reject_bad_arguments():
         Q.per_channel_scales(np.zeros((0, 4), np.float32), 127.0)
     assert ei.value.code == _lib.INVALID_ARG
     assert b"bad dims" in _lib.lib().nflow_last_error()
+
+
+def test_layer_handles_reject_bad_arguments():
+    """Argument checks of the layer-handle entry points run before any device
+    call (null pointers, dims, format), returning InvalidArg as the
+    reference's checks do (int8_gemm.cpp:203-208)."""
+    import ctypes as C
+    L = _lib.lib()
+    h = C.c_void_p(1234)
+    W = np.ones((4, 8), np.float32)
+    wp = W.ctypes.data_as(C.c_void_p)
+    assert L.nflow_layer_create(None, None, 4, 8, 0, C.byref(h)) == _lib.INVALID_ARG
+    assert h.value is None                     # the handle is cleared on failure
+    assert L.nflow_layer_create(wp, None, 0, 8, 0, C.byref(h)) == _lib.INVALID_ARG
+    assert L.nflow_layer_create(wp, None, 4, -1, 0, C.byref(h)) == _lib.INVALID_ARG
+    assert L.nflow_layer_create(wp, None, 4, 8, 7, C.byref(h)) == _lib.INVALID_ARG
+    assert b"format" in L.nflow_last_error()
+    assert L.nflow_layer_create(wp, None, 4, 8, 0, None) == _lib.INVALID_ARG
+    assert L.nflow_layer_create_int8(None, None, None, None, None, 4, 8, C.byref(h)) == _lib.INVALID_ARG
+    assert L.nflow_layer_forward(None, 10, None, None, None, 0, None) == _lib.INVALID_ARG
+    assert L.nflow_layer_shape(None, None, None, None) == _lib.INVALID_ARG
+    assert L.nflow_layer_destroy(None) == _lib.OK
