@@ -20,7 +20,9 @@ static void launch_gemm_t(const RowsArgs& a, hipStream_t st) {
     (void)attr;  // a failure surfaces as a launch error
     using S = GemmShape<TM, TN>;
     const int64_t blocks = ((a.M + S::BM - 1) / S::BM) * ((a.N + S::BN - 1) / S::BN);
-    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, st, a);
+    // MI355X deals blocks round-robin to 8 XCDs of 32 CUs.
+    const int groups = num_cus() % 8 == 0 ? 8 : 1;
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, st, a, groups);
 }
 
 // Tile shape: 128 x 256 for large M and N (two blocks per CU), else

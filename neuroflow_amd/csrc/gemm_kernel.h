@@ -53,8 +53,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, in
 // accumulators in all 256 AGPRs (one wave per SIMD); smaller tiles fit two.
 constexpr int gemm_min_waves(int TM, int TN) { return TM * TN >= 64 ? 1 : 2; }
 
+// Tile of block `bid` among `nblk`: blocks are dealt round-robin to `groups`
+// XCDs (block b runs on XCD b % groups, each with its own L2), so XCD x is
+// given the contiguous tile range [x q + min(x, rem), ...) of its
+// q + (x < rem) blocks (q = nblk / groups, rem = nblk % groups).  The N tiles
+// of one row tile then run together behind one L2 and share its A rows.
+__device__ __forceinline__ int gemm_tile_of_block(int bid, int nblk, int groups) {
+    const int x = bid % groups, s = bid / groups;
+    const int q = nblk / groups, rem = nblk % groups;
+    return x * q + (x < rem ? x : rem) + s;
+}
+
 template <int TM, int TN, int OUT, int ACT>
-__global__ __launch_bounds__(256, gemm_min_waves(TM, TN)) void k_gemm(RowsArgs a) {
+__global__ __launch_bounds__(256, gemm_min_waves(TM, TN)) void k_gemm(RowsArgs a, int xcd_groups) {
     using S = GemmShape<TM, TN>;
     constexpr int BM = S::BM, BN = S::BN;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -73,10 +84,11 @@ __global__ __launch_bounds__(256, gemm_min_waves(TM, TN)) void k_gemm(RowsArgs a
     const int K = a.K;
     const int64_t M = a.M;
     const int N = a.N;
-    // Block order: consecutive blocks share an A row tile (N tiles inner).
+    // Tile order: consecutive tiles share an A row tile (N tiles inner).
     const int n_tiles = (N + BN - 1) / BN;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.x / n_tiles) * BM;
-    const int n0 = static_cast<int>(blockIdx.x % n_tiles) * BN;
+    const int tile = gemm_tile_of_block(blockIdx.x, gridDim.x, xcd_groups);
+    const int64_t m0 = static_cast<int64_t>(tile / n_tiles) * BM;
+    const int n0 = static_cast<int>(tile % n_tiles) * BN;
 
     const auto rs_a = rows_rsrc(a.Aq, m0, M, BM, K);
     const auto rs_w = rows_rsrc(a.W, n0, N, BN, K);
