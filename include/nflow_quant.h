@@ -150,6 +150,15 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
                                         const float* A, float* C, float* scale_A_out,
                                         int activation, void* stream);
 
+/* The FNO local-linear layer (cpp/src/fno.cpp:515-557, 650-654):
+ * y = act(x1 + x2) with x2 = the per-token layer above (bias included) and
+ * x1 (M, out_features) the spectral branch, in the operation order of the
+ * reference (x2 = (scale_W * scale_A) * float(t) + bias, then x1 + x2, then
+ * the activation).  x1 and y are device buffers that must not be the same. */
+int nflow_int8_fno_layer_per_token(const nflow_int8_linear_params* p, int64_t M, const float* h,
+                                   const float* x1, float* y, float* scale_A_out, int activation,
+                                   void* stream);
+
 /* Raw int32 accumulators: C[m][n] = sum_k A_q[m][k] * W_q[n][k]. */
 int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, int K,
                         int32_t* C, void* stream);
@@ -189,6 +198,12 @@ int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q,
 int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M,
                                        const float* A, float* C, float* scale_A_out,
                                        int activation, void* stream);
+
+/* The FNO local-linear layer on the FP8 path: y = act(x1 + x2), x2 the
+ * per-token FP8 layer above (see nflow_int8_fno_layer_per_token). */
+int nflow_fp8_fno_layer_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* h,
+                                  const float* x1, float* y, float* scale_A_out, int activation,
+                                  void* stream);
 
 /* fp32 accumulators of the FP8 GEMM: C[m][n] = sum_k dec(A_q[m][k]) * dec(W_q[n][k]). */
 int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K,
@@ -248,6 +263,10 @@ int nflow_layer_create_int8(const int8_t* W_q, const float* scale_W, const int32
  * nflow_fp8_linear_forward_per_token with the handle's blob. */
 int nflow_layer_forward(const nflow_layer* layer, int64_t M, const float* x, float* y,
                         float* scale_A_out, int activation, void* stream);
+
+/* The FNO layer form act(x1 + x2) on a handle (see nflow_int8_fno_layer_per_token). */
+int nflow_layer_forward_residual(const nflow_layer* layer, int64_t M, const float* x, const float* x1,
+                                 float* y, float* scale_A_out, int activation, void* stream);
 
 int nflow_layer_shape(const nflow_layer* layer, int* out_features, int* in_features, int* format);
 

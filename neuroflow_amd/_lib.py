@@ -68,6 +68,7 @@ SIGNATURES = {
     "nflow_int8_linear_forward_batched": [_P8, _i64, _vp, _vp, _vp],
     "nflow_int8_quantise_per_token": [_vp, _i64, _i32, _vp, _vp, _vp, _vp],
     "nflow_int8_linear_forward_per_token": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
+    "nflow_int8_fno_layer_per_token": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
     "nflow_int8_gemm_i32": [_vp, _vp, _i64, _i32, _i32, _vp, _vp],
     "nflow_int8_linear_forward_quantised": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_fp8_e4m3_to_bits": [_vp, _vp, _i64, _vp],
@@ -75,6 +76,7 @@ SIGNATURES = {
     "nflow_fp8_e4m3_fake_quant": [_vp, _f32, _vp, _i64, _vp],
     "nflow_fp8_quantise_per_token": [_vp, _i64, _i32, _vp, _vp, _vp],
     "nflow_fp8_linear_forward_per_token": [_PF8, _i64, _vp, _vp, _vp, _i32, _vp],
+    "nflow_fp8_fno_layer_per_token": [_PF8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
     "nflow_fp8_gemm_f32": [_vp, _vp, _i64, _i32, _i32, _vp, _vp],
     "nflow_fp8_linear_forward_quantised": [_PF8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_host_quantise_weight_2d": [_vp, _i32, _i32, _vp, _vp, _vp, _vp],
@@ -83,6 +85,7 @@ SIGNATURES = {
     "nflow_layer_create": [_vp, _vp, _i32, _i32, _i32, C.POINTER(_vp)],
     "nflow_layer_create_int8": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(_vp)],
     "nflow_layer_forward": [_vp, _i64, _vp, _vp, _vp, _i32, _vp],
+    "nflow_layer_forward_residual": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
     "nflow_layer_shape": [_vp, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)],
     "nflow_layer_destroy": [_vp],
 }

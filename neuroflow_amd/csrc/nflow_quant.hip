@@ -217,6 +217,14 @@ __global__ __launch_bounds__(256) void k_quantise_rows(const float* __restrict__
     }
 }
 
+// The FNO layer's h = act(x1 + x2) (fno.cpp:650-654) over a finished x2 in C.
+__global__ __launch_bounds__(256) void k_residual_act(float* __restrict__ C, const float* __restrict__ R,
+                                                      int64_t n, int act) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        C[i] = activate_rt(R[i] + C[i], act);
+}
+
 // ---------------------------------------------------------------------------
 // Launch helpers
 // ---------------------------------------------------------------------------
@@ -388,16 +396,22 @@ int nflow_int8_quantise_per_token(const float* A, int64_t M, int K, int8_t* A_q,
     return check_launch("quantise_per_token");
 }
 
-int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64_t M,
-                                        const float* A, float* C, float* scale_A_out,
-                                        int activation, void* stream) {
-    clear_error();
+}  // extern "C"
+
+namespace nfq {
+
+// Per-token INT8 layer; with a residual R (M x N) the result is the FNO layer
+// form act(R + x2): fused in the K = N = 64 kernel, else x2 then one pass.
+static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const float* A,
+                          const float* R, float* C, float* scale_A_out, int activation,
+                          void* stream) {
     if (!A || !C || !p || !p->W_int8 || !p->scale_W)
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: null input/output");
     if (p->in_features <= 0 || p->out_features <= 0)
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: bad feature dims");
     if (!valid_act(activation))
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: unknown activation");
+    if (R && R == C) return set_error(NFLOW_INVALID_ARG, "fno_layer: x1 and y must be distinct buffers");
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
     RowsArgs a{};
@@ -415,17 +429,24 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
     a.kb_dot = kb_dot_for(a.formula, a.K);
     a.C = C;
     a.scale_out = scale_A_out;
-    if (rows64_ok(a) && !getenv_flag("NFLOW_NO_ROWS64")) {
+    if (rows64_ok(a) && (!R || aligned(R, 16)) && !getenv_flag("NFLOW_NO_ROWS64")) {
+        a.residual = R;
         launch_rows64<false>(a, activation, st);
         return check_launch("linear_forward_per_token");
     }
+    const int act_x2 = R ? static_cast<int>(ACT_NONE) : activation;
+    auto finish = [&]() {
+        if (R) hipLaunchKernelGGL(k_residual_act, dim3(grid_for(M * a.N, 256, 16)), dim3(256), 0, st, C, R,
+                                  M * a.N, activation);
+        return check_launch("linear_forward_per_token");
+    };
     // Wide K: quantise into a workspace, then the tiled GEMM (below).
     RowsArgs g = a;
     g.Aq = nullptr;  // the codes go to the workspace, which is 256-byte aligned
     const bool wide = use_gemm(g);
     if (!wide && rows_ok(a, IN_F32_TOKEN)) {
-        launch_rows<false, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
-        return check_launch("linear_forward_per_token");
+        launch_rows<false, IN_F32_TOKEN, OUT_EPI>(a, act_x2, st);
+        return finish();
     }
     // Split path: quantise into a workspace, then the product.
     const size_t codes = static_cast<size_t>(M) * a.K;
@@ -437,10 +458,28 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
     if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
     a.Aq = q;
     a.scale_in = sc;
-    if (wide) launch_gemm<OUT_EPI>(a, activation, st);
-    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, st);
-    else launch_generic<false, OUT_EPI>(a, activation, st);
-    return check_launch("linear_forward_per_token");
+    if (wide) launch_gemm<OUT_EPI>(a, act_x2, st);
+    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, act_x2, st);
+    else launch_generic<false, OUT_EPI>(a, act_x2, st);
+    return finish();
+}
+
+}  // namespace nfq
+
+extern "C" {
+
+int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64_t M,
+                                        const float* A, float* C, float* scale_A_out,
+                                        int activation, void* stream) {
+    clear_error();
+    return int8_per_token(p, M, A, nullptr, C, scale_A_out, activation, stream);
+}
+
+int nflow_int8_fno_layer_per_token(const nflow_int8_linear_params* p, int64_t M, const float* h,
+                                   const float* x1, float* y, float* scale_A_out, int activation,
+                                   void* stream) {
+    clear_error();
+    return int8_per_token(p, M, h, x1, y, scale_A_out, activation, stream);
 }
 
 int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, int K, int32_t* C,
@@ -540,12 +579,16 @@ static int fp8_check(const nflow_fp8_linear_params* p, int act, const char* what
     return NFLOW_OK;
 }
 
-int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A,
-                                       float* C, float* scale_A_out, int activation, void* stream) {
-    clear_error();
+}  // extern "C"
+
+namespace nfq {
+
+static int fp8_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A, const float* R,
+                         float* C, float* scale_A_out, int activation, void* stream) {
     if (!A || !C) return set_error(NFLOW_INVALID_ARG, "fp8_linear_forward_per_token: null input/output");
     int rc = fp8_check(p, activation, "fp8_linear_forward_per_token");
     if (rc) return rc;
+    if (R && R == C) return set_error(NFLOW_INVALID_ARG, "fp8_fno_layer: x1 and y must be distinct buffers");
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
     RowsArgs a{};
@@ -559,13 +602,20 @@ int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t
     a.kb_dot = (a.K + 63) / 64;
     a.C = C;
     a.scale_out = scale_A_out;
-    if (rows64_ok(a) && !getenv_flag("NFLOW_NO_ROWS64")) {
+    if (rows64_ok(a) && (!R || aligned(R, 16)) && !getenv_flag("NFLOW_NO_ROWS64")) {
+        a.residual = R;
         launch_rows64<true>(a, activation, st);
         return check_launch("fp8_linear_forward_per_token");
     }
-    if (rows_ok(a, IN_F32_TOKEN)) {
-        launch_rows<true, IN_F32_TOKEN, OUT_EPI>(a, activation, st);
+    const int act_x2 = R ? static_cast<int>(ACT_NONE) : activation;
+    auto finish = [&]() {
+        if (R) hipLaunchKernelGGL(k_residual_act, dim3(grid_for(M * a.N, 256, 16)), dim3(256), 0, st, C, R,
+                                  M * a.N, activation);
         return check_launch("fp8_linear_forward_per_token");
+    };
+    if (rows_ok(a, IN_F32_TOKEN)) {
+        launch_rows<true, IN_F32_TOKEN, OUT_EPI>(a, act_x2, st);
+        return finish();
     }
     const size_t codes = static_cast<size_t>(M) * a.K;
     Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float), st);
@@ -576,9 +626,26 @@ int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t
     if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
     a.Aq = q;
     a.scale_in = sc;
-    if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_EPI>(a, activation, st);
-    else launch_generic<true, OUT_EPI>(a, activation, st);
-    return check_launch("fp8_linear_forward_per_token");
+    if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_EPI>(a, act_x2, st);
+    else launch_generic<true, OUT_EPI>(a, act_x2, st);
+    return finish();
+}
+
+}  // namespace nfq
+
+extern "C" {
+
+int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A,
+                                       float* C, float* scale_A_out, int activation, void* stream) {
+    clear_error();
+    return fp8_per_token(p, M, A, nullptr, C, scale_A_out, activation, stream);
+}
+
+int nflow_fp8_fno_layer_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* h,
+                                  const float* x1, float* y, float* scale_A_out, int activation,
+                                  void* stream) {
+    clear_error();
+    return fp8_per_token(p, M, h, x1, y, scale_A_out, activation, stream);
 }
 
 int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K, float* C,

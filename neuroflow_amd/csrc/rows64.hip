@@ -14,29 +14,31 @@ bool rows64_ok(const RowsArgs& a) {
 #define NFQ_ROWS64_PF 1
 #endif
 
-template <bool FP8, int ACT>
+template <bool FP8, int ACT, bool RES>
 static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
-    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF>;
+    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES>;
     static const int per_cu = resident_blocks(kern);
     // Persistent waves that all take the same number of tiles (to within
     // one): the fewest waves that keep the per-wave count of a full grid.
     const int64_t tiles = (a.M + 15) / 16;
-#ifdef NFQ_ROWS64_TILES_PER_WAVE
-    const int64_t per_wave = NFQ_ROWS64_TILES_PER_WAVE;
-    (void)per_cu;
-#else
     const int64_t slots = static_cast<int64_t>(num_cus()) * per_cu * 4;
     const int64_t per_wave = (tiles + slots - 1) / slots;
-#endif
     const int64_t waves = (tiles + per_wave - 1) / per_wave;
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, st, a);
 }
 
+template <bool FP8, bool RES>
+static void launch_rows64_res(const RowsArgs& a, int act, hipStream_t st) {
+    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU, RES>(a, st);
+    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH, RES>(a, st);
+    else launch_rows64_act<FP8, ACT_NONE, RES>(a, st);
+}
+
+// a.residual (M x 64, 16-byte aligned) selects the FNO layer form act(x1 + x2).
 template <bool FP8>
 void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
-    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU>(a, st);
-    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH>(a, st);
-    else launch_rows64_act<FP8, ACT_NONE>(a, st);
+    if (a.residual) launch_rows64_res<FP8, true>(a, act, st);
+    else launch_rows64_res<FP8, false>(a, act, st);
 }
 
 template void launch_rows64<false>(const RowsArgs&, int, hipStream_t);

@@ -131,7 +131,8 @@ __device__ __attribute__((noinline)) uint32_t pack4_token_scale(v4f v, float s) 
                  quant_i8_token(v[2], s, inv), quant_i8_token(v[3], s, inv));
 }
 
-template <bool FP8, int ACT, int PF = 1>
+// RES: the FNO layer form act(x1 + x2) with x1 = a.residual (fno.cpp:650-654).
+template <bool FP8, int ACT, int PF = 1, bool RES = false>
 __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     constexpr bool INT_EPI = !FP8;
     using L = Rows64Lds<FP8>;
@@ -216,6 +217,15 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) pre[p][j] = pre[p + 1][j];
         load_lin(tile + PF * nwaves, pre[PF - 1]);
+        // Residual tile in the MFMA result layout: lane (r, g), column tile
+        // nt -> row r, columns 16 nt + 4 g .. + 3.
+        v4f res[4];
+        if constexpr (RES) {
+            const auto rr = tile_rsrc(a.residual, tile * 16, M, 256);
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                res[nt] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rr, (r * 64 + 16 * nt + 4 * g) * 4, 0, 0));
+        }
 
         // Row absmax in the linear layout: amax[j] = absmax of row 4j + lr.
         float amax[4];
@@ -379,7 +389,11 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             const v4f bb = lds_b[4 * nt + g];
             v4f y;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) y[v] = activate<ACT>(dequant_bias(sw[v], s_r, t[v], bb[v]));
+            for (int v = 0; v < 4; ++v) {
+                const float x2 = dequant_bias(sw[v], s_r, t[v], bb[v]);
+                if constexpr (RES) y[v] = activate<ACT>(res[nt][v] + x2);
+                else y[v] = activate<ACT>(x2);
+            }
             *reinterpret_cast<v4f*>(my.out + r * L::OUT_STRIDE + 16 * nt + 4 * g) = y;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -81,6 +81,7 @@ struct RowsArgs {
     int kb_dot;             // number of 64-wide K blocks that enter the dot
     void* C;                // (M, N) fp32 (OUT_EPI, FP8 OUT_RAW) or int32 (INT8 OUT_RAW)
     float* scale_out;       // (M) or null: per-row scales (IN_F32_TOKEN)
+    const float* residual;  // (M, N) or null: added before the activation (FNO layer)
 };
 
 // Operand dwords per lane per 64-wide K block: 16 int8 codes, or 16 bf16.

@@ -285,6 +285,34 @@ def fp8_linear_forward_per_token(p: Fp8LinearParams, A: torch.Tensor, activation
     return (out, s) if return_scales else out
 
 
+def _fno(fn_name, p, h, x1, activation, out, return_scales, what):
+    _dev(h, torch.float32, "h")
+    _dev(x1, torch.float32, "x1")
+    ps = p.c_struct()
+    M = _rows(h, p.in_features)
+    if x1.shape[-1] != p.out_features or x1.numel() != M * p.out_features:
+        raise ValueError("x1 must be (M, out_features)")
+    if out is None:
+        out = torch.empty(*h.shape[:-1], p.out_features, dtype=torch.float32, device=h.device)
+    s = torch.empty(M, dtype=torch.float32, device=h.device) if return_scales else None
+    check(getattr(_lib.lib(), fn_name)(C.byref(ps), M, _p(h), _p(x1), _p(out), _p(s), _act(activation),
+                                       _stream()), what)
+    return (out, s) if return_scales else out
+
+
+def fno_layer_per_token(p: Int8LinearParams, h: torch.Tensor, x1: torch.Tensor, activation="gelu",
+                        out: Optional[torch.Tensor] = None, return_scales: bool = False):
+    """The FNO local-linear layer act(x1 + (W q(h) + b)) with per-token INT8
+    (fno.cpp:515-557, 650-654); x1 is the spectral branch, (M, out_features)."""
+    return _fno("nflow_int8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fno_layer")
+
+
+def fp8_fno_layer_per_token(p: Fp8LinearParams, h: torch.Tensor, x1: torch.Tensor, activation="gelu",
+                            out: Optional[torch.Tensor] = None, return_scales: bool = False):
+    """fno_layer_per_token on the FP8 E4M3 path."""
+    return _fno("nflow_fp8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fp8_fno_layer")
+
+
 def fp8_gemm_f32(A_q: torch.Tensor, W_q: torch.Tensor) -> torch.Tensor:
     _dev(A_q, torch.uint8, "A_q")
     _dev(W_q, torch.uint8, "W_q")
@@ -468,7 +496,8 @@ class Layer:
         return cls(_handle=h)
 
     def __call__(self, x: torch.Tensor, activation="gelu", out: Optional[torch.Tensor] = None,
-                 return_scales: bool = False):
+                 return_scales: bool = False, residual: Optional[torch.Tensor] = None):
+        """act(W q(x) + b), or with `residual` x1 the FNO form act(x1 + (W q(x) + b))."""
         _dev(x, torch.float32, "x")
         if x.shape[-1] != self.in_features:
             raise ValueError(f"x has {x.shape[-1]} features, the layer takes {self.in_features}")
@@ -476,9 +505,17 @@ class Layer:
         if out is None:
             out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.float32, device=x.device)
         s = torch.empty(M, dtype=torch.float32, device=x.device) if return_scales else None
-        check(_lib.lib().nflow_layer_forward(self._h, M, x.data_ptr(), out.data_ptr(),
-                                             None if s is None else s.data_ptr(), _act(activation),
-                                             _stream()), "layer_forward")
+        sp = None if s is None else s.data_ptr()
+        if residual is None:
+            check(_lib.lib().nflow_layer_forward(self._h, M, x.data_ptr(), out.data_ptr(), sp,
+                                                 _act(activation), _stream()), "layer_forward")
+        else:
+            _dev(residual, torch.float32, "residual")
+            if residual.numel() != M * self.out_features:
+                raise ValueError("residual must be (M, out_features)")
+            check(_lib.lib().nflow_layer_forward_residual(self._h, M, x.data_ptr(), residual.data_ptr(),
+                                                          out.data_ptr(), sp, _act(activation), _stream()),
+                  "layer_forward_residual")
         return (out, s) if return_scales else out
 
     def close(self) -> None:
