@@ -80,6 +80,16 @@ __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32
     return lo | hi;
 }
 
+// DPP row moves (16-lane rows): the lane pattern CTRL of v within each row.
+template <int CTRL>
+__device__ __forceinline__ int dpp_movi(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, dpp_movi<CTRL>(__builtin_bit_cast(int, v)));
+}
+
 // Sum of the four signed bytes of a dword (v_dot4_i32_i8 against ones).
 __device__ __forceinline__ int32_t sum_bytes_i8(uint32_t v, int32_t acc) {
     return __builtin_amdgcn_sdot4(static_cast<int>(v), 0x01010101, acc, false);

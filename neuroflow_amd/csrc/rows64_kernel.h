@@ -22,13 +22,6 @@
 
 namespace nfq {
 
-// DPP row move (16-lane rows).
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
 // Absmax over the 16 lanes of a DPP row of four-float chunks, NaN operands
 // ignored and starting from 0 (the reference's `if (a > m) m = a` loop):
 // fmaxf, so every step canonicalises.  The exact path uses it.

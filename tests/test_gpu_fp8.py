@@ -49,7 +49,8 @@ def test_decode_and_fake_quant(gpu):
     assert np.array_equal(Q.fp8_e4m3_to_bits(x[:100]), O.e4m3_encode(x[:100]))
 
 
-@pytest.mark.parametrize("M,K", [(1, 64), (999, 64), (100, 256), (10, 100), (70, 1024), (5, 4096)])
+@pytest.mark.parametrize("M,K", [(1, 64), (999, 64), (100, 256), (10, 100), (70, 1024), (5, 4096),
+                                 (33, 512), (20001, 256)])
 def test_quantise_per_token_fp8(gpu, M, K):
     x = 2.0 * WL.normal(31, (M, K))
     x[0, :4] = [1e-4, -1e-5, 448.0, 0.0]
@@ -133,7 +134,7 @@ def test_fp8_layer_k64_special_rows(gpu, act):
     np.testing.assert_allclose(out[fin], exact[fin], rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("K", [256, 1024])
+@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
 def test_quantise_per_token_fp8_special_rows(gpu, K):
     """The register-resident quantise (K = 256 KV) on zero, NaN, signalling
     NaN, infinite, subnormal and saturating rows: scales and bytes bit-exact."""

@@ -37,7 +37,7 @@ def _weights(N, K, sid, zp=False):
 
 
 @pytest.mark.parametrize("M,K", [(1, 64), (37, 64), (1000, 64), (513, 256), (77, 100), (64, 1024),
-                                 (33, 4)])
+                                 (33, 4), (31, 512), (66, 1024), (20001, 256), (3, 2048)])
 def test_quantise_per_token_codes_bit_exact(gpu, M, K):
     A = WL.normal(11, (M, K)) * 3.0
     A[0, 0] = 0.0
@@ -67,7 +67,7 @@ def test_quantise_per_token_ties_and_specials(gpu):
     assert np.array_equal(_host(q), q_ref)
 
 
-@pytest.mark.parametrize("K", [256, 1024])
+@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
 def test_quantise_per_token_special_rows_wide(gpu, K):
     """The register-resident quantise (K = 256 KV) on exact ties, zero, NaN,
     signalling NaN, infinite and subnormal rows: codes, scales and sums."""
