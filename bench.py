@@ -74,7 +74,11 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     """Average duration of the tiled GEMM kernel alone (codes in, fused
     epilogue out) for layer 0, on per-token codes prepared outside the timed
     region; launches go through the C entry point with a prebuilt struct so
-    that Python overhead stays off the GPU's critical path."""
+    that Python overhead stays off the GPU's critical path.  The layer's
+    weights are per-channel symmetric (zero points 0, sum_W equal to the
+    codes' own sums), so the struct leaves zp_W and sum_W out: the GEMM then
+    needs no byte sums and runs the same LDS-DMA kernel as the layer, with
+    identical outputs."""
     import ctypes as C
     import torch
     from neuroflow_amd import _lib
@@ -83,7 +87,9 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     M, N = wl.M, L.W.shape[0]
     codes = [Q.quantise_per_token(s_[0]) for s_ in sets]
     outs = [torch.empty(M, N, dtype=torch.float32, device=sets[0][0].device) for _ in sets]
-    ps = obj.params.c_struct()
+    import dataclasses
+    assert not obj.params.zp_W.any().item()
+    ps = dataclasses.replace(obj.params, zp_W=None, sum_W_per_row=None).c_struct()
     fn = _lib.lib().nflow_int8_linear_forward_quantised
     act = {"none": 0, "relu": 1, "gelu": 2}[L.act]
     sptr = stream.cuda_stream

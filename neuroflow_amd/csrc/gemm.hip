@@ -38,9 +38,34 @@ static int gemm_shape(const RowsArgs& a) {
     return (a.M >= 16384 && a.N >= 1024) ? 48 : 44;
 }
 
+template <int TM, int TN, int OUT, int ACT>
+static void launch_pipe_t(const RowsArgs& a, hipStream_t st) {
+    using S = GemmShape<TM, TN>;
+    const int64_t blocks = ((a.M + S::BM - 1) / S::BM) * ((a.N + S::BN - 1) / S::BN);
+    const int groups = num_cus() % 8 == 0 ? 8 : 1;
+    hipLaunchKernelGGL((k_gemm_pipe<TM, TN, OUT, ACT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, a,
+                       groups);
+}
+
+// The LDS-DMA kernel takes every case whose epilogue needs no byte sums of
+// its own: zp_A = 0, row sums given when zero points may be nonzero, and
+// weight-row sums given when the row-VNNI formula has a caller's sum_W.
+bool gemm_pipe_ok(const RowsArgs& a, int out) {
+    if (a.zp_A != 0 || getenv_flag("NFLOW_GEMM_REG")) return false;
+    if (out == OUT_RAW) return true;
+    const bool need_colsum = a.formula == F_ROW_VNNI && a.sumW;
+    return (!a.zpW || a.sum_in) && (!need_colsum || a.colsum_in);
+}
+
 template <int OUT, int ACT>
 static void launch_gemm_act(const RowsArgs& a, hipStream_t st) {
-    switch (gemm_shape(a)) {
+    const int shape = gemm_shape(a);
+    if (shape != 88 && gemm_pipe_ok(a, OUT)) {
+        if (shape == 48) launch_pipe_t<4, 8, OUT, ACT>(a, st);
+        else launch_pipe_t<4, 4, OUT, ACT>(a, st);
+        return;
+    }
+    switch (shape) {
         case 88: launch_gemm_t<8, 8, OUT, ACT>(a, st); break;
         case 48: launch_gemm_t<4, 8, OUT, ACT>(a, st); break;
         default: launch_gemm_t<4, 4, OUT, ACT>(a, st); break;

@@ -81,6 +81,8 @@ void launch_rows64(const RowsArgs& a, int act, hipStream_t st);
 
 // The tiled MFMA GEMM on INT8 codes for K a multiple of 64, K >= 128 (gemm.hip).
 bool gemm_ok(const RowsArgs& a);
+// Whether launch_gemm takes the LDS-DMA kernel for `a` (out: OUT_EPI / OUT_RAW).
+bool gemm_pipe_ok(const RowsArgs& a, int out);
 template <int OUT>
 void launch_gemm(const RowsArgs& a, int act, hipStream_t st);
 

@@ -38,11 +38,52 @@ __global__ __launch_bounds__(256) void k_quantise_fixed(const float* __restrict_
 }
 
 // One wave per row: absmax -> scale -> codes (+ sum of codes).
+// Weight-row byte sums the tiled GEMM's row-VNNI term needs next to a
+// caller's sum_W (int8_gemm.cpp:386-393), formed by the quantise launch that
+// runs just before the GEMM instead of a launch of their own.  out == null:
+// none wanted.
+struct CodeSums {
+    const uint8_t* W;   // (N, K) int8 codes, 16-byte aligned rows
+    int N;
+    int K;              // a multiple of 16
+    int32_t* out;       // (N)
+};
+
+// Rows 4 wg .. 4 wg + 3 of cs.W: 16 lanes per row, DPP row reductions.
+__device__ __forceinline__ void code_sums_group(const CodeSums& cs, int64_t wg) {
+    const int lane = threadIdx.x & 63, c = lane & 15;
+    const int64_t n = wg * 4 + (lane >> 4);
+    int32_t acc = 0;
+    if (n < cs.N) {
+        const v4u* w = reinterpret_cast<const v4u*>(cs.W + n * cs.K);
+        for (int j = c; j < cs.K / 16; j += 16) {
+            const v4u v = w[j];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = sum_bytes_i8(v[q], acc);
+        }
+    }
+    acc += dpp_movi<0xB1>(acc);   // quad_perm [1,0,3,2]
+    acc += dpp_movi<0x4E>(acc);   // quad_perm [2,3,0,1]
+    acc += dpp_movi<0x141>(acc);  // row_half_mirror
+    acc += dpp_movi<0x140>(acc);  // row_mirror
+    if (c == 0 && n < cs.N) cs.out[n] = acc;
+}
+
+// Every wave of a quantise launch first takes its share of the weight rows.
+__device__ __forceinline__ void code_sums_share(const CodeSums& cs) {
+    if (!cs.out) return;
+    const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t wg = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); wg * 4 < cs.N; wg += nw)
+        code_sums_group(cs, wg);
+}
+
 template <bool FP8>
 __global__ __launch_bounds__(256) void k_quantise_token(const float* __restrict__ A, int64_t M,
                                                         int K, uint8_t* __restrict__ Aq,
                                                         float* __restrict__ scale,
-                                                        int32_t* __restrict__ sum_a) {
+                                                        int32_t* __restrict__ sum_a,
+                                                        CodeSums cs) {
+    code_sums_share(cs);
     const int lane = threadIdx.x & 63;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
     for (int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); m < M; m += nw) {
@@ -87,6 +128,10 @@ __global__ __launch_bounds__(256) void k_sum_w(const int8_t* __restrict__ W,
     for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s);
     if (lane == 0) out[o] = static_cast<int32_t>(acc);
 }
+
+// The weight-row byte sums on their own (linear_forward_quantised, which has
+// no quantise launch to carry them).
+__global__ __launch_bounds__(256) void k_code_sums(CodeSums cs) { code_sums_share(cs); }
 
 __global__ __launch_bounds__(256) void k_e4m3_encode(const float* __restrict__ in,
                                                      uint8_t* __restrict__ out, int64_t n) {
@@ -174,7 +219,9 @@ template <bool FP8, int KV>
 __global__ __launch_bounds__(256) void k_quantise_rows(const float* __restrict__ A, int64_t M,
                                                        uint8_t* __restrict__ Aq,
                                                        float* __restrict__ scale,
-                                                       int32_t* __restrict__ sum_a) {
+                                                       int32_t* __restrict__ sum_a,
+                                                       CodeSums cs) {
+    code_sums_share(cs);
     constexpr int K = 256 * KV;
     const int lane = threadIdx.x & 63;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
@@ -228,7 +275,9 @@ template <bool FP8, int KV>
 __global__ __launch_bounds__(256) void k_quantise_rows16(const float* __restrict__ A, int64_t M,
                                                          uint8_t* __restrict__ Aq,
                                                          float* __restrict__ scale,
-                                                         int32_t* __restrict__ sum_a) {
+                                                         int32_t* __restrict__ sum_a,
+                                                         CodeSums cs) {
+    code_sums_share(cs);
     constexpr int K = 256 * KV, J = 4 * KV;
     const int lane = threadIdx.x & 63, c = lane & 15;
     const int64_t nw = static_cast<int64_t>(gridDim.x) * 4;
@@ -304,7 +353,8 @@ static void launch_generic(const RowsArgs& a, int act, hipStream_t st) {
 // row with a loop over K.
 template <bool FP8>
 static void launch_quantise_token(const float* A, int64_t M, int K, uint8_t* Aq, float* scale,
-                                  int32_t* sum_a, hipStream_t st) {
+                                  int32_t* sum_a, hipStream_t st,
+                                  CodeSums cs = CodeSums{nullptr, 0, 0, nullptr}) {
     const dim3 grid(grid_for(M, 4, 16)), block(256);
     if (aligned(A, 16) && aligned(Aq, 4)) {
         // K <= 512: 16 lanes per row, a block takes 16 rows, 4 blocks per CU.
@@ -313,15 +363,15 @@ static void launch_quantise_token(const float* A, int64_t M, int K, uint8_t* Aq,
         // (measured on MI355X at M = 65536, K = 1024: 68 us against 64 us).
         const dim3 grid16(grid_for(M, 16, 4));
         switch (K) {
-            case 256: hipLaunchKernelGGL((k_quantise_rows16<FP8, 1>), grid16, block, 0, st, A, M, Aq, scale, sum_a); return;
-            case 512: hipLaunchKernelGGL((k_quantise_rows16<FP8, 2>), grid16, block, 0, st, A, M, Aq, scale, sum_a); return;
-            case 1024: hipLaunchKernelGGL((k_quantise_rows<FP8, 4>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
-            case 2048: hipLaunchKernelGGL((k_quantise_rows<FP8, 8>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
-            case 4096: hipLaunchKernelGGL((k_quantise_rows<FP8, 16>), grid, block, 0, st, A, M, Aq, scale, sum_a); return;
+            case 256: hipLaunchKernelGGL((k_quantise_rows16<FP8, 1>), grid16, block, 0, st, A, M, Aq, scale, sum_a, cs); return;
+            case 512: hipLaunchKernelGGL((k_quantise_rows16<FP8, 2>), grid16, block, 0, st, A, M, Aq, scale, sum_a, cs); return;
+            case 1024: hipLaunchKernelGGL((k_quantise_rows<FP8, 4>), grid, block, 0, st, A, M, Aq, scale, sum_a, cs); return;
+            case 2048: hipLaunchKernelGGL((k_quantise_rows<FP8, 8>), grid, block, 0, st, A, M, Aq, scale, sum_a, cs); return;
+            case 4096: hipLaunchKernelGGL((k_quantise_rows<FP8, 16>), grid, block, 0, st, A, M, Aq, scale, sum_a, cs); return;
             default: break;
         }
     }
-    hipLaunchKernelGGL((k_quantise_token<FP8>), grid, block, 0, st, A, M, K, Aq, scale, sum_a);
+    hipLaunchKernelGGL((k_quantise_token<FP8>), grid, block, 0, st, A, M, K, Aq, scale, sum_a, cs);
 }
 
 static int check_launch(const char* what) {
@@ -518,15 +568,25 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
         return finish();
     }
     // Split path: quantise into a workspace, then the product.
+    // Workspace: codes, then M scales; for the tiled GEMM, M row code sums
+    // from the same quantise pass when zero points may be nonzero, and N
+    // weight-row byte sums when the formula takes a caller's sum_W.
     const size_t codes = static_cast<size_t>(M) * a.K;
-    Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float), st);
+    const bool want_sums = wide && a.zpW;
+    const bool want_colsum = wide && a.formula == F_ROW_VNNI && a.sumW;
+    const size_t n_sums = (want_sums ? static_cast<size_t>(M) : 0) + (want_colsum ? a.N : 0);
+    Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float) + n_sums * sizeof(int32_t), st);
     if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_per_token: workspace allocation failed");
     uint8_t* q = static_cast<uint8_t*>(ws.p);
     float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
-    launch_quantise_token<false>(A, M, a.K, q, sc, static_cast<int32_t*>(nullptr), st);
+    int32_t* sums = want_sums ? reinterpret_cast<int32_t*>(sc + M) : nullptr;
+    int32_t* colsum = want_colsum ? reinterpret_cast<int32_t*>(sc + M) + (want_sums ? M : 0) : nullptr;
+    launch_quantise_token<false>(A, M, a.K, q, sc, sums, st, CodeSums{a.W, a.N, a.K, colsum});
     if (scale_A_out) (void)hipMemcpyAsync(scale_A_out, sc, sizeof(float) * M, hipMemcpyDeviceToDevice, st);
     a.Aq = q;
     a.scale_in = sc;
+    a.sum_in = sums;
+    a.colsum_in = colsum;
     if (wide) launch_gemm<OUT_EPI>(a, act_x2, st);
     else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, act_x2, st);
     else launch_generic<false, OUT_EPI>(a, act_x2, st);
@@ -597,9 +657,26 @@ int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64
     a.formula = formula_row(a.K);
     a.kb_dot = kb_dot_for(a.formula, a.K);
     a.C = C;
-    if (use_gemm(a)) launch_gemm<OUT_EPI>(a, activation, as_stream(stream));
-    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
-    else launch_generic<false, OUT_EPI>(a, activation, as_stream(stream));
+    hipStream_t st = as_stream(stream);
+    if (use_gemm(a)) {
+        // Without zero points a caller's sum_W only needs the weight-row
+        // byte sums (a pre-pass) to keep the GEMM on its LDS-DMA kernel.
+        if (!a.zpW && a.formula == F_ROW_VNNI && a.sumW) {
+            Scratch ws(static_cast<size_t>(a.N) * sizeof(int32_t), st);
+            if (ws.err != hipSuccess)
+                return set_error(NFLOW_INTERNAL, "linear_forward_quantised: workspace allocation failed");
+            int32_t* colsum = static_cast<int32_t*>(ws.p);
+            hipLaunchKernelGGL(k_code_sums, dim3(grid_for(a.N, 16, 4)), dim3(256), 0, st, CodeSums{a.W, a.N, a.K, colsum});
+            a.colsum_in = colsum;
+            launch_gemm<OUT_EPI>(a, activation, st);
+            return check_launch("linear_forward_quantised");
+        }
+        launch_gemm<OUT_EPI>(a, activation, st);
+    } else if (rows_ok(a, IN_CODES)) {
+        launch_rows<false, IN_CODES, OUT_EPI>(a, activation, st);
+    } else {
+        launch_generic<false, OUT_EPI>(a, activation, st);
+    }
     return check_launch("linear_forward_quantised");
 }
 

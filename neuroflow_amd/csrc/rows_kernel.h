@@ -82,6 +82,8 @@ struct RowsArgs {
     void* C;                // (M, N) fp32 (OUT_EPI, FP8 OUT_RAW) or int32 (INT8 OUT_RAW)
     float* scale_out;       // (M) or null: per-row scales (IN_F32_TOKEN)
     const float* residual;  // (M, N) or null: added before the activation (FNO layer)
+    const int32_t* sum_in;     // IN_CODES: (M) row code sums, or null (the tiled GEMM only)
+    const int32_t* colsum_in;  // (N) byte sums of W's rows over K, or null (the tiled GEMM only)
 };
 
 // Operand dwords per lane per 64-wide K block: 16 int8 codes, or 16 bf16.

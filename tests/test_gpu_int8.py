@@ -157,6 +157,25 @@ def test_quantised_entry_matches_fused(gpu):
     assert _bits_equal(y1[:64], ref)
 
 
+@pytest.mark.parametrize("zp_none", [False, True])
+@pytest.mark.parametrize("sum_mode", ["none", "own", "off"])
+def test_quantised_entry_param_forms(gpu, zp_none, sum_mode):
+    """linear_forward_quantised with and without zp_W / sum_W (the GEMM picks
+    its kernel from them; a sum_W off the weights' own sums enters the
+    formula verbatim)."""
+    M, N, K = 3000, 512, 320
+    A = WL.normal(24, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 25)
+    sumW = {"none": None, "own": sw, "off": (sw + 3).astype(np.int32)}[sum_mode]
+    p = Q.Int8LinearParams(_cu(q), _cu(s), None if zp_none else _cu(zps), _cu(b),
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    Aq, sa, _ = Q.quantise_per_token(_cu(A))
+    y = _host(Q.linear_forward_quantised(p, Aq, sa, "none"))
+    rows = np.unique(np.concatenate([np.arange(0, M, 29), [M - 1]]))
+    ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, 0)
+    assert _bits_equal(y[rows], ref)
+
+
 def test_precompute_sum_w(gpu):
     _, q, s, zps, sw, b = _weights(300, 200, 22, zp=True)
     got = _host(Q.precompute_sum_w(_cu(q), _cu(zps)))
@@ -237,7 +256,7 @@ def test_fused_k64_layer_asymmetric_weights(gpu):
 # ---- the tiled GEMM (K a multiple of 64, K >= 128): every tile shape ----------
 
 # (M, N, K) choosing the 256x256, 128x256 and 128x128 block tiles on 256 CUs.
-GEMM_SHAPES = [(16384, 1024, 256), (8192, 1024, 128), (2000, 200, 192), (1, 64, 128)]
+GEMM_SHAPES = [(16384, 1024, 256), (8192, 1024, 128), (2000, 200, 192), (1, 64, 128), (500, 256, 320)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
@@ -286,4 +305,19 @@ def test_gemm_layer_asymmetric_weights(gpu, M, N, K, with_sum):
     out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
     rows = np.unique(np.concatenate([np.arange(0, M, 13), [M - 1]]))
     ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, 0)
+    assert _bits_equal(out[rows], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 256, 256), (16384, 1024, 320), (64, 1024, 1024)])
+def test_gemm_layer_given_sum_w_not_matching(gpu, M, N, K):
+    """A caller-given sum_W_per_row that is not the weights' byte sum enters
+    the row-VNNI formula verbatim (int8_gemm.cpp:386-393): the tiled GEMM must
+    then form each column's own byte sum to reproduce it."""
+    A = WL.normal(36, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 37)
+    sw_bad = (sw + np.arange(N, dtype=np.int32) % 11 - 5).astype(np.int32)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw_bad))
+    out = _host(Q.linear_forward_per_token(p, _cu(A), "relu"))
+    rows = np.unique(np.concatenate([np.arange(0, M, 17), [M - 1]]))
+    ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sw_bad, 1)
     assert _bits_equal(out[rows], ref)
