@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define NFLOW_QUANT_ABI_VERSION 2
+#define NFLOW_QUANT_ABI_VERSION 3
 
 /* nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37. */
 enum nflow_status_code {
@@ -268,10 +268,78 @@ int nflow_layer_forward(const nflow_layer* layer, int64_t M, const float* x, flo
 int nflow_layer_forward_residual(const nflow_layer* layer, int64_t M, const float* x, const float* x1,
                                  float* y, float* scale_A_out, int activation, void* stream);
 
+/* The per-tensor INT8 layer of the IR-driven FNO path: LinearForwardBatched
+ * with the handle's blob and the input's per-tensor (scale_A, zp_A), bias
+ * added after the dequantisation (cpp/src/fno.cpp:135-156, 541-549);
+ * INT8 handles only, M <= INT32_MAX. */
+int nflow_layer_forward_per_tensor(const nflow_layer* layer, int64_t M, const float* x, float* y,
+                                   float scale_A, int32_t zp_A, void* stream);
+
 int nflow_layer_shape(const nflow_layer* layer, int* out_features, int* in_features, int* format);
 
 /* Frees the handle and its device memory (NULL is allowed). */
 int nflow_layer_destroy(nflow_layer* layer);
+
+/* ---- NeuroIR binary + NIRQ block (HOST memory) -------------------------
+ * Replaces ir_native::LoadBinary (cpp/include/neuroflow/ir_loader.h:58-654)
+ * for what the device path needs: the header, every weight record and the
+ * NIRQ qparams (kinds 0-3, ir_loader.h:556-650).  Status codes as the
+ * reference: FileNotFound, ParseError, UnsupportedOp (unknown op code).
+ * Weight names are not checked against the op's fixed order.  Pointers
+ * returned by the accessors live until nflow_ir_close. */
+typedef struct nflow_ir nflow_ir;
+
+enum nflow_qparam_kind {
+    NFLOW_QPARAM_PER_TENSOR = 0,
+    NFLOW_QPARAM_PER_CHANNEL = 1,
+    NFLOW_QPARAM_PER_TOKEN = 2,
+    NFLOW_QPARAM_FP8_E4M3 = 3
+};
+
+int nflow_ir_open(const char* path, nflow_ir** ir);
+int nflow_ir_open_memory(const void* data, size_t bytes, nflow_ir** ir);
+int nflow_ir_close(nflow_ir* ir);
+
+/* version 1-3; op_code 1-8 (FNO1d, FNO2d, FNO3d, DeepONet, TokenMixer,
+ * GraphOp, TokenMixer2D, GraphOp2D); config8: the 7 or 8 config int32s, zero
+ * padded; activation 0 gelu / 1 relu; quant_enabled: a NIRQ block was read.
+ * Any output pointer may be NULL. */
+int nflow_ir_header(const nflow_ir* ir, int* version, int* op_code, int32_t* config8, int* activation,
+                    int* quant_enabled);
+int nflow_ir_num_weights(const nflow_ir* ir, int* n);
+/* Weight record `index` in file order; dims8 holds up to 8 dims. */
+int nflow_ir_weight_at(const nflow_ir* ir, int index, const char** name, int* ndim, int64_t* dims8,
+                       const float** data);
+/* Weight by name (the first record of that name); InvalidArg if absent. */
+int nflow_ir_weight(const nflow_ir* ir, const char* name, int* ndim, int64_t* dims8, const float** data);
+
+/* Qparam records in file order (duplicates included) ... */
+int nflow_ir_num_qparams(const nflow_ir* ir, int* n);
+int nflow_ir_qparam_at(const nflow_ir* ir, int index, const char** name, int* kind);
+/* ... and lookups by name, as the reference's maps (the last record of a
+ * name wins; a per-tensor name ending in ".output" is an activation qparam,
+ * any other a weight qparam).  *found = 0 when absent. */
+int nflow_ir_per_tensor_qparam(const nflow_ir* ir, const char* name, int* found, float* scale, int32_t* zp);
+int nflow_ir_per_channel_qparam(const nflow_ir* ir, const char* name, int* found, int* n_channels, int* axis,
+                                const float** scales, const int32_t** zero_points);
+int nflow_ir_per_token_qparam(const nflow_ir* ir, const char* name, int* found, int* n_tokens, int* width,
+                              const float** scales, const int32_t** zero_points);
+int nflow_ir_fp8_qparam(const nflow_ir* ir, const char* name, int* found, float* scale);
+
+/* EnableInt8Gemm for one weight (cpp/src/fno.cpp:325-406): QuantiseWeight2D
+ * with the IR's per-channel scales and zero points of `weight_name` (a 2-D
+ * weight, channel axis 0), uploaded once with the IR weight `bias_name`
+ * (NULL: no bias) as a device-resident INT8 layer handle. */
+int nflow_ir_layer_create(const nflow_ir* ir, const char* weight_name, const char* bias_name,
+                          nflow_layer** layer);
+
+/* LinearDispatchTryInt8's decision for the FNO layer locs.{layer_index}
+ * once EnableInt8Gemm has run (cpp/src/fno.cpp:125-159, 529-536): INT8 iff
+ * its input key (lift.output for layer 0, else locs.{i-1}.output) has no
+ * per-token or FP8 qparam, locs.{i}.weight would be cached, and the input
+ * key has a per-tensor qparam, whose scale / zero point are returned. */
+int nflow_ir_fno_int8_dispatch(const nflow_ir* ir, int layer_index, int* use_int8, float* scale_A,
+                               int32_t* zp_A);
 
 #ifdef __cplusplus
 }

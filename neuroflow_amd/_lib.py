@@ -86,8 +86,29 @@ SIGNATURES = {
     "nflow_layer_create_int8": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(_vp)],
     "nflow_layer_forward": [_vp, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_layer_forward_residual": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "nflow_layer_forward_per_tensor": [_vp, _i64, _vp, _vp, _f32, C.c_int32, _vp],
     "nflow_layer_shape": [_vp, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)],
     "nflow_layer_destroy": [_vp],
+    "nflow_ir_open": [C.c_char_p, C.POINTER(_vp)],
+    "nflow_ir_open_memory": [_vp, C.c_size_t, C.POINTER(_vp)],
+    "nflow_ir_close": [_vp],
+    "nflow_ir_header": [_vp, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(C.c_int32), C.POINTER(_i32),
+                        C.POINTER(_i32)],
+    "nflow_ir_num_weights": [_vp, C.POINTER(_i32)],
+    "nflow_ir_weight_at": [_vp, _i32, C.POINTER(C.c_char_p), C.POINTER(_i32), C.POINTER(C.c_int64),
+                           C.POINTER(_vp)],
+    "nflow_ir_weight": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(C.c_int64), C.POINTER(_vp)],
+    "nflow_ir_num_qparams": [_vp, C.POINTER(_i32)],
+    "nflow_ir_qparam_at": [_vp, _i32, C.POINTER(C.c_char_p), C.POINTER(_i32)],
+    "nflow_ir_per_tensor_qparam": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(C.c_float),
+                                   C.POINTER(C.c_int32)],
+    "nflow_ir_per_channel_qparam": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32),
+                                    C.POINTER(_vp), C.POINTER(_vp)],
+    "nflow_ir_per_token_qparam": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32),
+                                  C.POINTER(_vp), C.POINTER(_vp)],
+    "nflow_ir_fp8_qparam": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(C.c_float)],
+    "nflow_ir_layer_create": [_vp, C.c_char_p, C.c_char_p, C.POINTER(_vp)],
+    "nflow_ir_fno_int8_dispatch": [_vp, _i32, C.POINTER(_i32), C.POINTER(C.c_float), C.POINTER(C.c_int32)],
 }
 _RESTYPES = {"nflow_last_error": C.c_char_p}
 

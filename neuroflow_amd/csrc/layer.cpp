@@ -7,6 +7,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <climits>
 #include <cstring>
 #include <new>
 #include <string>
@@ -159,6 +160,19 @@ int nflow_layer_forward_residual(const nflow_layer* layer, int64_t M, const floa
     const nflow_fp8_linear_params p{static_cast<const uint8_t*>(layer->W), layer->scale_W, layer->bias,
                                     layer->in_features, layer->out_features};
     return nflow_fp8_fno_layer_per_token(&p, M, x, x1, y, scale_A_out, activation, stream);
+}
+
+int nflow_layer_forward_per_tensor(const nflow_layer* layer, int64_t M, const float* x, float* y, float scale_A,
+                                   int32_t zp_A, void* stream) {
+    clear_error();
+    if (!layer) return set_error(NFLOW_INVALID_ARG, "layer_forward_per_tensor: null layer");
+    if (layer->format != NFLOW_FORMAT_INT8)
+        return set_error(NFLOW_UNSUPPORTED_OP, "layer_forward_per_tensor: INT8 layers only");
+    if (M > INT32_MAX) return set_error(NFLOW_INVALID_ARG, "layer_forward_per_tensor: M exceeds the batched API's int");
+    const nflow_int8_linear_params p{static_cast<const int8_t*>(layer->W), layer->scale_W, layer->zp_W,
+                                     layer->bias, layer->in_features, layer->out_features, scale_A, zp_A,
+                                     layer->sum_W};
+    return nflow_int8_linear_forward_batched(&p, static_cast<int>(M), x, y, stream);
 }
 
 int nflow_layer_shape(const nflow_layer* layer, int* out_features, int* in_features, int* format) {

@@ -1,0 +1,135 @@
+"""NeuroIR binary files (.nneuroir) with their NIRQ quantisation block, read
+by libnflow_quant (ir_native::LoadBinary, cpp/include/neuroflow/ir_loader.h:
+58-654), and the IR-driven device layers of FNO1d::EnableInt8Gemm
+(cpp/src/fno.cpp:325-406) and LinearDispatchTryInt8 (fno.cpp:125-159)."""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+from typing import Dict, List, Optional, Tuple, Union
+
+import numpy as np
+
+from . import _lib
+from ._lib import check
+
+OPS = {1: "FNO1d", 2: "FNO2d", 3: "FNO3d", 4: "DeepONet", 5: "TokenMixer", 6: "GraphOp",
+       7: "TokenMixer2D", 8: "GraphOp2D"}
+QPARAM_KINDS = {0: "per_tensor", 1: "per_channel", 2: "per_token", 3: "fp8_e4m3"}
+
+
+def _arr(ptr: int, n: int, ctype) -> np.ndarray:
+    if n == 0:
+        return np.zeros(0, np.dtype(ctype))
+    return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ctype)), shape=(n,)).copy()
+
+
+class IR:
+    """An opened IR file: IR(path) or IR(data=bytes)."""
+
+    def __init__(self, path: Union[str, Path, None] = None, data: Optional[bytes] = None):
+        self._h = C.c_void_p()
+        L = _lib.lib()
+        if (path is None) == (data is None):
+            raise ValueError("give exactly one of path or data")
+        if path is not None:
+            check(L.nflow_ir_open(str(path).encode(), C.byref(self._h)), "ir_open")
+        else:
+            buf = C.create_string_buffer(bytes(data), len(data))
+            check(L.nflow_ir_open_memory(buf, len(data), C.byref(self._h)), "ir_open_memory")
+        v, op, act, q = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        cfg = (C.c_int32 * 8)()
+        check(L.nflow_ir_header(self._h, C.byref(v), C.byref(op), cfg, C.byref(act), C.byref(q)), "ir_header")
+        self.version, self.op_code = v.value, op.value
+        self.op = OPS[op.value]
+        self.config = list(cfg)
+        self.activation = "relu" if act.value == 1 else "gelu"
+        self.quant_enabled = bool(q.value)
+
+    def weight_names(self) -> List[str]:
+        n = C.c_int()
+        check(_lib.lib().nflow_ir_num_weights(self._h, C.byref(n)), "ir_num_weights")
+        names = []
+        for i in range(n.value):
+            nm = C.c_char_p()
+            check(_lib.lib().nflow_ir_weight_at(self._h, i, C.byref(nm), None, None, None), "ir_weight_at")
+            names.append(nm.value.decode())
+        return names
+
+    def weight(self, name: str) -> np.ndarray:
+        nd = C.c_int()
+        dims = (C.c_int64 * 8)()
+        data = C.c_void_p()
+        check(_lib.lib().nflow_ir_weight(self._h, name.encode(), C.byref(nd), dims, C.byref(data)), "ir_weight")
+        shape = tuple(dims[i] for i in range(nd.value))
+        return _arr(data.value, int(np.prod(shape, dtype=np.int64)), C.c_float).reshape(shape)
+
+    def qparam_records(self) -> List[Tuple[str, str]]:
+        n = C.c_int()
+        check(_lib.lib().nflow_ir_num_qparams(self._h, C.byref(n)), "ir_num_qparams")
+        out = []
+        for i in range(n.value):
+            nm, k = C.c_char_p(), C.c_int()
+            check(_lib.lib().nflow_ir_qparam_at(self._h, i, C.byref(nm), C.byref(k)), "ir_qparam_at")
+            out.append((nm.value.decode(), QPARAM_KINDS[k.value]))
+        return out
+
+    def per_tensor(self, name: str) -> Optional[Tuple[float, int]]:
+        f, s, z = C.c_int(), C.c_float(), C.c_int32()
+        check(_lib.lib().nflow_ir_per_tensor_qparam(self._h, name.encode(), C.byref(f), C.byref(s), C.byref(z)),
+              "ir_per_tensor_qparam")
+        return (s.value, z.value) if f.value else None
+
+    def per_channel(self, name: str) -> Optional[Tuple[np.ndarray, np.ndarray, int]]:
+        f, n, ax, sp, zp = C.c_int(), C.c_int(), C.c_int(), C.c_void_p(), C.c_void_p()
+        check(_lib.lib().nflow_ir_per_channel_qparam(self._h, name.encode(), C.byref(f), C.byref(n), C.byref(ax),
+                                                     C.byref(sp), C.byref(zp)), "ir_per_channel_qparam")
+        if not f.value:
+            return None
+        return _arr(sp.value, n.value, C.c_float), _arr(zp.value, n.value, C.c_int32), ax.value
+
+    def per_token(self, name: str) -> Optional[Tuple[np.ndarray, np.ndarray, int]]:
+        f, n, w, sp, zp = C.c_int(), C.c_int(), C.c_int(), C.c_void_p(), C.c_void_p()
+        check(_lib.lib().nflow_ir_per_token_qparam(self._h, name.encode(), C.byref(f), C.byref(n), C.byref(w),
+                                                   C.byref(sp), C.byref(zp)), "ir_per_token_qparam")
+        if not f.value:
+            return None
+        return _arr(sp.value, n.value, C.c_float), _arr(zp.value, n.value, C.c_int32), w.value
+
+    def fp8(self, name: str) -> Optional[float]:
+        f, s = C.c_int(), C.c_float()
+        check(_lib.lib().nflow_ir_fp8_qparam(self._h, name.encode(), C.byref(f), C.byref(s)), "ir_fp8_qparam")
+        return s.value if f.value else None
+
+    def layer(self, weight_name: str, bias_name: Optional[str] = None):
+        """EnableInt8Gemm for one weight: a device-resident INT8 quant.Layer."""
+        from .quant import Layer
+        h = C.c_void_p()
+        check(_lib.lib().nflow_ir_layer_create(self._h, weight_name.encode(),
+                                               None if bias_name is None else bias_name.encode(), C.byref(h)),
+              "ir_layer_create")
+        return Layer(_handle=h)
+
+    def fno_int8_dispatch(self, layer_index: int) -> Optional[Tuple[float, int]]:
+        """(scale_A, zp_A) when locs.{i} would run the INT8 GEMM, else None."""
+        use, s, z = C.c_int(), C.c_float(), C.c_int32()
+        check(_lib.lib().nflow_ir_fno_int8_dispatch(self._h, layer_index, C.byref(use), C.byref(s), C.byref(z)),
+              "ir_fno_int8_dispatch")
+        return (s.value, z.value) if use.value else None
+
+    def close(self) -> None:
+        if self._h:
+            _lib.lib().nflow_ir_close(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -518,6 +518,21 @@ class Layer:
                   "layer_forward_residual")
         return (out, s) if return_scales else out
 
+    def forward_per_tensor(self, x: torch.Tensor, scale_A: float, zp_A: int = 0,
+                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The IR-driven per-tensor INT8 layer: LinearForwardBatched with the
+        handle's blob, then + bias (fno.cpp:135-156, 541-549)."""
+        _dev(x, torch.float32, "x")
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"x has {x.shape[-1]} features, the layer takes {self.in_features}")
+        M = x.numel() // self.in_features
+        if out is None:
+            out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.float32, device=x.device)
+        check(_lib.lib().nflow_layer_forward_per_tensor(self._h, M, x.data_ptr(), out.data_ptr(),
+                                                        float(scale_A), int(zp_A), _stream()),
+              "layer_forward_per_tensor")
+        return out
+
     def close(self) -> None:
         if self._h:
             _lib.lib().nflow_layer_destroy(self._h)

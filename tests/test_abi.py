@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version_and_status_values():
-    assert _lib.lib().nflow_quant_abi_version() == 2
+    assert _lib.lib().nflow_quant_abi_version() == 3
     text = HEADER.read_text()
     # nflow::StatusCode, cpp/include/neuroflow/tensor.h:29-37
     for name, val in [("NFLOW_OK", 0), ("NFLOW_INVALID_ARG", 1), ("NFLOW_FILE_NOT_FOUND", 2),
