@@ -248,7 +248,7 @@ def main():
     if K0 == 64 and N0 == 64:
         kernel = "nfq::k_rows64"
     elif K0 % 64 == 0 and K0 >= 128 and wl.layers[0].fmt == "int8":
-        kernel = "nfq::k_gemm"     # after a per-token quantise launch
+        kernel = "nfq::k_gemm_pipe"     # after a per-token quantise launch
     else:
         kernel = "nfq::k_rows"
     roof.update({"kernel": kernel,
@@ -256,7 +256,7 @@ def main():
                  "bytes_per_launch": bytes_step // len(layers),
                  "ops_per_launch": ops_step // len(layers),
                  "tops": round(tops, 2), "gbs": round(gbs, 1)})
-    if kernel == "nfq::k_gemm":
+    if kernel == "nfq::k_gemm_pipe":
         # The layer is two launches (quantise, then the GEMM); the roofline
         # is the GEMM kernel's own, timed alone on layer 0's shape.
         g_us, g_bytes, g_ops = time_gemm_only(wl, layers, sets, stream, max(20, args.steps))
