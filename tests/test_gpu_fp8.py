@@ -150,3 +150,32 @@ def test_quantise_per_token_fp8_special_rows(gpu, K):
     q_ref, s_ref = O.quantise_per_token_fp8(x)
     assert np.array_equal(_host(s).view(np.uint32), s_ref.view(np.uint32))
     assert np.array_equal(_host(q), q_ref)
+
+
+@pytest.mark.parametrize("act", ["none", "relu"])
+def test_fp8_layer_k64_below_min_normal_cap(gpu, act):
+    """Quotients in (7 * 2^-9, 2^-6) and at the 7.5 * 2^-9 tie: the reference
+    encoder caps them at 7 * 2^-9 (fp8_e4m3.h:192-211) where round-to-nearest
+    reaches 2^-6.  The large element sits on a zero weight column so the
+    outputs stay small enough that one wrong E4M3 value breaks 1e-5 / 1e-6."""
+    M, K, N = 64, 64, 64
+    rng = np.random.default_rng(7)
+    x = np.zeros((M, K), np.float32)
+    x[:, 0] = 448.0                                 # absmax -> scale 1, 1 / scale = 1
+    grid = np.array([7.0, 7.125, 7.25, 7.5, 7.75, 7.875, 7.99, 6.5, 6.75, 7.5, 8.0, 8.5], np.float32) * 2.0 ** -9
+    for m in range(M):
+        vals = rng.choice(grid, K - 1) * rng.choice([-1.0, 1.0], K - 1)
+        x[m, 1:] = vals.astype(np.float32)
+    W = WL.uniform(41, (N, K), -0.125, 0.125)
+    W[:, 0] = 0.0
+    b = np.zeros(N, np.float32)
+    layer = Q.Fp8Linear(W, b)
+    out = _host(layer(_cu(x), act))
+    a = {"none": 0, "relu": 1}[act]
+    qa, sa = O.quantise_per_token_fp8(x)
+    assert np.all(sa == 1.0)
+    exact = O.layer_fp8_exact(qa, sa, layer.W_q, layer.scale_W, b, a)
+    np.testing.assert_allclose(out, exact, rtol=RTOL, atol=ATOL)
+    # The same layer with the capped values replaced by 2^-6 must differ.
+    dec = O.e4m3_decode(qa)
+    assert np.any(np.abs(dec) == 7.0 * 2.0 ** -9)
