@@ -189,6 +189,39 @@ int nflow_fp8_e4m3_fake_quant(const float* in, float scale, float* out, int64_t 
 int nflow_fp8_quantise_per_token(const float* A, int64_t M, int K, uint8_t* A_q,
                                  float* scale_A, void* stream);
 
+/* The optional static fake-quant of x2 in the FNO layer (cpp/src/fno.cpp:
+ * 572-648), INT8 forms: q = clamp(std::round(x2 / s) + zp, -128, 127) in
+ * float, x2 = (q - zp) * s, applied after the bias and before x1 + x2.
+ * PER_POSITION follows the reference's indexing: at that point x2 is laid
+ * out (batch, width, points) but the loop addresses it as (batch, points,
+ * width), so qparam p applies to flat offset p of a sample's (width, points)
+ * plane.  For the token-major layer (row m = sample * points + position,
+ * column j) that is index j * points + m % points.  The log2 "FP8" snap of
+ * fno.cpp:579-606 is not an E4M3 operation and is not offered. */
+enum nflow_x2_quant_kind {
+    NFLOW_X2_NONE = 0,
+    NFLOW_X2_PER_TENSOR = 1,
+    NFLOW_X2_PER_POSITION = 2,
+    NFLOW_X2_FP8_LOG2 = 3 /* reported by nflow_ir_fno_x2_quant; the layers reject it */
+};
+
+typedef struct nflow_x2_quant {
+    int kind;                   /* enum nflow_x2_quant_kind */
+    float scale;                /* PER_TENSOR (and FP8_LOG2) */
+    int32_t zero_point;         /* PER_TENSOR */
+    const float* scales;        /* PER_POSITION: n_positions scales (device memory for the layers) */
+    const int32_t* zero_points; /* PER_POSITION: n_positions zero points */
+    int64_t n_positions;        /* PER_POSITION: at least out_features * points */
+    int32_t width;              /* PER_POSITION: the qparam's width; must equal out_features */
+    int32_t points;             /* PER_POSITION: grid points per sample (rows per sample) */
+} nflow_x2_quant;
+
+/* nflow_int8_fno_layer_per_token with the x2 fake-quant x2q (NULL or kind
+ * NONE: none); x1 may be NULL (no residual term). */
+int nflow_int8_fno_layer_per_token_x2q(const nflow_int8_linear_params* p, int64_t M, const float* h,
+                                       const float* x1, float* y, float* scale_A_out, int activation,
+                                       const nflow_x2_quant* x2q, void* stream);
+
 /* Fused FP8 layer: per-token FP8 quantise -> GEMM on the matrix cores with
  * fp32 accumulation (E4M3 values are exact in bfloat16, so the product runs
  * as bf16 MFMA on exact operands) -> (scale_W[n] * scale_A[m]) * acc +
@@ -204,6 +237,11 @@ int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t
 int nflow_fp8_fno_layer_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* h,
                                   const float* x1, float* y, float* scale_A_out, int activation,
                                   void* stream);
+
+/* nflow_fp8_fno_layer_per_token with the x2 fake-quant (see nflow_x2_quant). */
+int nflow_fp8_fno_layer_per_token_x2q(const nflow_fp8_linear_params* p, int64_t M, const float* h,
+                                      const float* x1, float* y, float* scale_A_out, int activation,
+                                      const nflow_x2_quant* x2q, void* stream);
 
 /* fp32 accumulators of the FP8 GEMM: C[m][n] = sum_k dec(A_q[m][k]) * dec(W_q[n][k]). */
 int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K,
@@ -267,6 +305,10 @@ int nflow_layer_forward(const nflow_layer* layer, int64_t M, const float* x, flo
 /* The FNO layer form act(x1 + x2) on a handle (see nflow_int8_fno_layer_per_token). */
 int nflow_layer_forward_residual(const nflow_layer* layer, int64_t M, const float* x, const float* x1,
                                  float* y, float* scale_A_out, int activation, void* stream);
+
+/* The FNO layer on a handle with the x2 fake-quant; x1 may be NULL. */
+int nflow_layer_forward_fno(const nflow_layer* layer, int64_t M, const float* x, const float* x1, float* y,
+                            float* scale_A_out, int activation, const nflow_x2_quant* x2q, void* stream);
 
 /* The per-tensor INT8 layer of the IR-driven FNO path: LinearForwardBatched
  * with the handle's blob and the input's per-tensor (scale_A, zp_A), bias
@@ -340,6 +382,13 @@ int nflow_ir_layer_create(const nflow_ir* ir, const char* weight_name, const cha
  * key has a per-tensor qparam, whose scale / zero point are returned. */
 int nflow_ir_fno_int8_dispatch(const nflow_ir* ir, int layer_index, int* use_int8, float* scale_A,
                                int32_t* zp_A);
+
+/* The x2 fake-quant the reference applies to locs.{layer_index}'s output
+ * when the IR carries a qparam for "locs.{i}.output" (fno.cpp:572-648), with
+ * its precedence: FP8 (kind FP8_LOG2, scale only), else per-token (kind
+ * PER_POSITION; scales / zero_points point into the IR, host memory; points
+ * is left 0 for the caller), else per-tensor, else NONE. */
+int nflow_ir_fno_x2_quant(const nflow_ir* ir, int layer_index, nflow_x2_quant* x2q);
 
 #ifdef __cplusplus
 }

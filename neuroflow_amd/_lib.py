@@ -53,6 +53,22 @@ class Fp8LinearParamsC(C.Structure):
     ]
 
 
+class X2QuantC(C.Structure):
+    """nflow_x2_quant (include/nflow_quant.h)."""
+    _fields_ = [
+        ("kind", C.c_int),
+        ("scale", C.c_float),
+        ("zero_point", C.c_int32),
+        ("scales", C.c_void_p),
+        ("zero_points", C.c_void_p),
+        ("n_positions", C.c_int64),
+        ("width", C.c_int32),
+        ("points", C.c_int32),
+    ]
+
+
+X2_NONE, X2_PER_TENSOR, X2_PER_POSITION, X2_FP8_LOG2 = 0, 1, 2, 3
+
 _vp, _i64, _i32, _f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
 _P8 = C.POINTER(Int8LinearParamsC)
 _PF8 = C.POINTER(Fp8LinearParamsC)
@@ -69,6 +85,7 @@ SIGNATURES = {
     "nflow_int8_quantise_per_token": [_vp, _i64, _i32, _vp, _vp, _vp, _vp],
     "nflow_int8_linear_forward_per_token": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_int8_fno_layer_per_token": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "nflow_int8_fno_layer_per_token_x2q": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, C.POINTER(X2QuantC), _vp],
     "nflow_int8_gemm_i32": [_vp, _vp, _i64, _i32, _i32, _vp, _vp],
     "nflow_int8_linear_forward_quantised": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_fp8_e4m3_to_bits": [_vp, _vp, _i64, _vp],
@@ -77,6 +94,7 @@ SIGNATURES = {
     "nflow_fp8_quantise_per_token": [_vp, _i64, _i32, _vp, _vp, _vp],
     "nflow_fp8_linear_forward_per_token": [_PF8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_fp8_fno_layer_per_token": [_PF8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "nflow_fp8_fno_layer_per_token_x2q": [_PF8, _i64, _vp, _vp, _vp, _vp, _i32, C.POINTER(X2QuantC), _vp],
     "nflow_fp8_gemm_f32": [_vp, _vp, _i64, _i32, _i32, _vp, _vp],
     "nflow_fp8_linear_forward_quantised": [_PF8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_host_quantise_weight_2d": [_vp, _i32, _i32, _vp, _vp, _vp, _vp],
@@ -86,6 +104,7 @@ SIGNATURES = {
     "nflow_layer_create_int8": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, C.POINTER(_vp)],
     "nflow_layer_forward": [_vp, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_layer_forward_residual": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
+    "nflow_layer_forward_fno": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, C.POINTER(X2QuantC), _vp],
     "nflow_layer_forward_per_tensor": [_vp, _i64, _vp, _vp, _f32, C.c_int32, _vp],
     "nflow_layer_shape": [_vp, C.POINTER(_i32), C.POINTER(_i32), C.POINTER(_i32)],
     "nflow_layer_destroy": [_vp],
@@ -109,6 +128,7 @@ SIGNATURES = {
     "nflow_ir_fp8_qparam": [_vp, C.c_char_p, C.POINTER(_i32), C.POINTER(C.c_float)],
     "nflow_ir_layer_create": [_vp, C.c_char_p, C.c_char_p, C.POINTER(_vp)],
     "nflow_ir_fno_int8_dispatch": [_vp, _i32, C.POINTER(_i32), C.POINTER(C.c_float), C.POINTER(C.c_int32)],
+    "nflow_ir_fno_x2_quant": [_vp, _i32, C.POINTER(X2QuantC)],
 }
 _RESTYPES = {"nflow_last_error": C.c_char_p}
 

@@ -263,6 +263,17 @@ __device__ __forceinline__ float int_epi_value(const IntEpi& e, int32_t D, int32
     return static_cast<float>(static_cast<int64_t>(static_cast<int32_t>(t32)) + e.c2);
 }
 
+// The FNO layer's INT8 fake-quant of x2 (fno.cpp:626-646 per-position,
+// :637-646 per-tensor): q = std::round(v / s) + zp in float (true division,
+// half away from zero), clamped to [-128, 127] (a NaN passes), then
+// (q - zp) * s.
+__device__ __forceinline__ float x2_fake_quant(float v, float s, float zpf) {
+    float q = roundf(v / s) + zpf;
+    q = q < -128.0f ? -128.0f : q;
+    q = q > 127.0f ? 127.0f : q;
+    return (q - zpf) * s;
+}
+
 // (scale_W[o] * scale_A) * float(t) + bias: the reference's operation order.
 __device__ __forceinline__ float dequant_bias(float sw, float sa, float t, float b) {
     const float s = sw * sa;

@@ -439,4 +439,34 @@ int nflow_ir_fno_int8_dispatch(const nflow_ir* ir, int layer_index, int* use_int
     return NFLOW_OK;
 }
 
+int nflow_ir_fno_x2_quant(const nflow_ir* ir, int layer_index, nflow_x2_quant* x2q) {
+    clear_error();
+    if (!ir || !x2q) return set_error(NFLOW_INVALID_ARG, "ir_fno_x2_quant: null argument");
+    if (layer_index < 0) return set_error(NFLOW_INVALID_ARG, "ir_fno_x2_quant: negative layer index");
+    *x2q = nflow_x2_quant{NFLOW_X2_NONE, 0.0f, 0, nullptr, nullptr, 0, 0, 0};
+    // fno.cpp:571-648: only with a NIRQ block; FP8 first, then per-token,
+    // then per-tensor, all keyed "locs.{i}.output".
+    if (!ir->quant_enabled) return NFLOW_OK;
+    const std::string key = "locs." + std::to_string(layer_index) + ".output";
+    if (auto f = ir->fp8.find(key); f != ir->fp8.end()) {
+        x2q->kind = NFLOW_X2_FP8_LOG2;
+        x2q->scale = f->second;
+        return NFLOW_OK;
+    }
+    if (auto t = ir->per_token.find(key); t != ir->per_token.end()) {
+        x2q->kind = NFLOW_X2_PER_POSITION;
+        x2q->scales = t->second.scales.data();
+        x2q->zero_points = t->second.zps.data();
+        x2q->n_positions = static_cast<int64_t>(t->second.scales.size());
+        x2q->width = t->second.width;
+        return NFLOW_OK;
+    }
+    if (auto q = ir->act_tensor.find(key); q != ir->act_tensor.end()) {
+        x2q->kind = NFLOW_X2_PER_TENSOR;
+        x2q->scale = q->second.scale;
+        x2q->zero_point = q->second.zp;
+    }
+    return NFLOW_OK;
+}
+
 }  // extern "C"

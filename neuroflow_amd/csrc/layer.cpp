@@ -162,6 +162,21 @@ int nflow_layer_forward_residual(const nflow_layer* layer, int64_t M, const floa
     return nflow_fp8_fno_layer_per_token(&p, M, x, x1, y, scale_A_out, activation, stream);
 }
 
+int nflow_layer_forward_fno(const nflow_layer* layer, int64_t M, const float* x, const float* x1, float* y,
+                            float* scale_A_out, int activation, const nflow_x2_quant* x2q, void* stream) {
+    clear_error();
+    if (!layer) return set_error(NFLOW_INVALID_ARG, "layer_forward_fno: null layer");
+    if (layer->format == NFLOW_FORMAT_INT8) {
+        const nflow_int8_linear_params p{static_cast<const int8_t*>(layer->W), layer->scale_W, layer->zp_W,
+                                         layer->bias, layer->in_features, layer->out_features, 1.0f, 0,
+                                         layer->sum_W};
+        return nflow_int8_fno_layer_per_token_x2q(&p, M, x, x1, y, scale_A_out, activation, x2q, stream);
+    }
+    const nflow_fp8_linear_params p{static_cast<const uint8_t*>(layer->W), layer->scale_W, layer->bias,
+                                    layer->in_features, layer->out_features};
+    return nflow_fp8_fno_layer_per_token_x2q(&p, M, x, x1, y, scale_A_out, activation, x2q, stream);
+}
+
 int nflow_layer_forward_per_tensor(const nflow_layer* layer, int64_t M, const float* x, float* y, float scale_A,
                                    int32_t zp_A, void* stream) {
     clear_error();

@@ -330,12 +330,27 @@ __global__ __launch_bounds__(256) void k_quantise_rows16(const float* __restrict
     }
 }
 
-// The FNO layer's h = act(x1 + x2) (fno.cpp:650-654) over a finished x2 in C.
-__global__ __launch_bounds__(256) void k_residual_act(float* __restrict__ C, const float* __restrict__ R,
-                                                      int64_t n, int act) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-        C[i] = activate_rt(R[i] + C[i], act);
+// The FNO layer's tail for the kernels that do not fuse it: C holds x2
+// (bias included); C = act(R + fq(x2)) with the optional x2 fake-quant of
+// a.xq_* (fno.cpp:572-654) and R (the spectral branch x1) optional.  One
+// block per row at a time, columns across the threads.
+__global__ __launch_bounds__(256) void k_fno_post(float* __restrict__ C, const float* __restrict__ R,
+                                                  RowsArgs a, int act) {
+    const int N = a.N;
+    for (int64_t m = blockIdx.x; m < a.M; m += gridDim.x) {
+        const int pos = a.xq_kind == 2 ? static_cast<int>(m % a.xq_points) : 0;
+        for (int j = threadIdx.x; j < N; j += blockDim.x) {
+            const int64_t i = m * N + j;
+            float x2 = C[i];
+            if (a.xq_kind == 1) {
+                x2 = x2_fake_quant(x2, a.xq_scale, a.xq_zpf);
+            } else if (a.xq_kind == 2) {
+                const int64_t idx = static_cast<int64_t>(j) * a.xq_points + pos;
+                x2 = x2_fake_quant(x2, a.xq_scales[idx], static_cast<float>(a.xq_zps[idx]));
+            }
+            C[i] = activate_rt(R ? R[i] + x2 : x2, act);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -521,9 +536,37 @@ namespace nfq {
 
 // Per-token INT8 layer; with a residual R (M x N) the result is the FNO layer
 // form act(R + x2): fused in the K = N = 64 kernel, else x2 then one pass.
+// The x2 fake-quant parameters into a (nflow_x2_quant, fno.cpp:572-648).
+static int apply_x2q(RowsArgs& a, const nflow_x2_quant* xq, const char* what) {
+    if (!xq || xq->kind == NFLOW_X2_NONE) return NFLOW_OK;
+    const std::string w(what);
+    if (xq->kind == NFLOW_X2_PER_TENSOR) {
+        a.xq_kind = 1;
+        a.xq_scale = xq->scale;
+        a.xq_zpf = static_cast<float>(xq->zero_point);
+        return NFLOW_OK;
+    }
+    if (xq->kind == NFLOW_X2_PER_POSITION) {
+        if (!xq->scales || !xq->zero_points) return set_error(NFLOW_INVALID_ARG, w + ": null per-position qparams");
+        if (xq->points <= 0) return set_error(NFLOW_INVALID_ARG, w + ": per-position qparams need points > 0");
+        if (xq->width != a.N)
+            return set_error(NFLOW_SHAPE_MISMATCH, w + ": per-position qparam width differs from out_features");
+        if (xq->n_positions < static_cast<int64_t>(a.N) * xq->points)
+            return set_error(NFLOW_SHAPE_MISMATCH, w + ": fewer per-position qparams than out_features * points");
+        a.xq_kind = 2;
+        a.xq_scales = xq->scales;
+        a.xq_zps = xq->zero_points;
+        a.xq_points = xq->points;
+        return NFLOW_OK;
+    }
+    if (xq->kind == NFLOW_X2_FP8_LOG2)
+        return set_error(NFLOW_UNSUPPORTED_OP, w + ": the log2 FP8 snap of x2 is not an E4M3 operation");
+    return set_error(NFLOW_INVALID_ARG, w + ": unknown x2 fake-quant kind");
+}
+
 static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const float* A,
                           const float* R, float* C, float* scale_A_out, int activation,
-                          void* stream) {
+                          const nflow_x2_quant* xq, void* stream) {
     if (!A || !C || !p || !p->W_int8 || !p->scale_W)
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: null input/output");
     if (p->in_features <= 0 || p->out_features <= 0)
@@ -531,13 +574,14 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
     if (!valid_act(activation))
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: unknown activation");
     if (R && R == C) return set_error(NFLOW_INVALID_ARG, "fno_layer: x1 and y must be distinct buffers");
+    RowsArgs a{};
+    a.N = p->out_features;
+    if (int rc = apply_x2q(a, xq, "fno_layer")) return rc;
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
-    RowsArgs a{};
     a.A = A;
     a.M = M;
     a.K = p->in_features;
-    a.N = p->out_features;
     a.W = reinterpret_cast<const uint8_t*>(p->W_int8);
     a.sW = p->scale_W;
     a.zpW = p->zp_W;
@@ -553,10 +597,10 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
         launch_rows64<false>(a, activation, st);
         return check_launch("linear_forward_per_token");
     }
-    const int act_x2 = R ? static_cast<int>(ACT_NONE) : activation;
+    const bool post = R || a.xq_kind;
+    const int act_x2 = post ? static_cast<int>(ACT_NONE) : activation;
     auto finish = [&]() {
-        if (R) hipLaunchKernelGGL(k_residual_act, dim3(grid_for(M * a.N, 256, 16)), dim3(256), 0, st, C, R,
-                                  M * a.N, activation);
+        if (post) hipLaunchKernelGGL(k_fno_post, dim3(grid_for(M, 1, 16)), dim3(256), 0, st, C, R, a, activation);
         return check_launch("linear_forward_per_token");
     };
     // Wide K: quantise into a workspace, then the tiled GEMM (below).
@@ -601,14 +645,21 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
                                         const float* A, float* C, float* scale_A_out,
                                         int activation, void* stream) {
     clear_error();
-    return int8_per_token(p, M, A, nullptr, C, scale_A_out, activation, stream);
+    return int8_per_token(p, M, A, nullptr, C, scale_A_out, activation, nullptr, stream);
 }
 
 int nflow_int8_fno_layer_per_token(const nflow_int8_linear_params* p, int64_t M, const float* h,
                                    const float* x1, float* y, float* scale_A_out, int activation,
                                    void* stream) {
     clear_error();
-    return int8_per_token(p, M, h, x1, y, scale_A_out, activation, stream);
+    return int8_per_token(p, M, h, x1, y, scale_A_out, activation, nullptr, stream);
+}
+
+int nflow_int8_fno_layer_per_token_x2q(const nflow_int8_linear_params* p, int64_t M, const float* h,
+                                       const float* x1, float* y, float* scale_A_out, int activation,
+                                       const nflow_x2_quant* x2q, void* stream) {
+    clear_error();
+    return int8_per_token(p, M, h, x1, y, scale_A_out, activation, x2q, stream);
 }
 
 int nflow_int8_gemm_i32(const int8_t* A_q, const int8_t* W_q, int64_t M, int N, int K, int32_t* C,
@@ -730,18 +781,20 @@ static int fp8_check(const nflow_fp8_linear_params* p, int act, const char* what
 namespace nfq {
 
 static int fp8_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A, const float* R,
-                         float* C, float* scale_A_out, int activation, void* stream) {
+                         float* C, float* scale_A_out, int activation, const nflow_x2_quant* xq,
+                         void* stream) {
     if (!A || !C) return set_error(NFLOW_INVALID_ARG, "fp8_linear_forward_per_token: null input/output");
     int rc = fp8_check(p, activation, "fp8_linear_forward_per_token");
     if (rc) return rc;
     if (R && R == C) return set_error(NFLOW_INVALID_ARG, "fp8_fno_layer: x1 and y must be distinct buffers");
+    RowsArgs a{};
+    a.N = p->out_features;
+    if (int rc2 = apply_x2q(a, xq, "fp8_fno_layer")) return rc2;
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
-    RowsArgs a{};
     a.A = A;
     a.M = M;
     a.K = p->in_features;
-    a.N = p->out_features;
     a.W = p->W_e4m3;
     a.sW = p->scale_W;
     a.bias = p->bias;
@@ -753,10 +806,10 @@ static int fp8_per_token(const nflow_fp8_linear_params* p, int64_t M, const floa
         launch_rows64<true>(a, activation, st);
         return check_launch("fp8_linear_forward_per_token");
     }
-    const int act_x2 = R ? static_cast<int>(ACT_NONE) : activation;
+    const bool post = R || a.xq_kind;
+    const int act_x2 = post ? static_cast<int>(ACT_NONE) : activation;
     auto finish = [&]() {
-        if (R) hipLaunchKernelGGL(k_residual_act, dim3(grid_for(M * a.N, 256, 16)), dim3(256), 0, st, C, R,
-                                  M * a.N, activation);
+        if (post) hipLaunchKernelGGL(k_fno_post, dim3(grid_for(M, 1, 16)), dim3(256), 0, st, C, R, a, activation);
         return check_launch("fp8_linear_forward_per_token");
     };
     if (rows_ok(a, IN_F32_TOKEN)) {
@@ -784,14 +837,21 @@ extern "C" {
 int nflow_fp8_linear_forward_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* A,
                                        float* C, float* scale_A_out, int activation, void* stream) {
     clear_error();
-    return fp8_per_token(p, M, A, nullptr, C, scale_A_out, activation, stream);
+    return fp8_per_token(p, M, A, nullptr, C, scale_A_out, activation, nullptr, stream);
 }
 
 int nflow_fp8_fno_layer_per_token(const nflow_fp8_linear_params* p, int64_t M, const float* h,
                                   const float* x1, float* y, float* scale_A_out, int activation,
                                   void* stream) {
     clear_error();
-    return fp8_per_token(p, M, h, x1, y, scale_A_out, activation, stream);
+    return fp8_per_token(p, M, h, x1, y, scale_A_out, activation, nullptr, stream);
+}
+
+int nflow_fp8_fno_layer_per_token_x2q(const nflow_fp8_linear_params* p, int64_t M, const float* h,
+                                      const float* x1, float* y, float* scale_A_out, int activation,
+                                      const nflow_x2_quant* x2q, void* stream) {
+    clear_error();
+    return fp8_per_token(p, M, h, x1, y, scale_A_out, activation, x2q, stream);
 }
 
 int nflow_fp8_gemm_f32(const uint8_t* A_q, const uint8_t* W_q, int64_t M, int N, int K, float* C,

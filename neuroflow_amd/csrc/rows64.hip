@@ -14,9 +14,9 @@ bool rows64_ok(const RowsArgs& a) {
 #define NFQ_ROWS64_PF 1
 #endif
 
-template <bool FP8, int ACT, bool RES>
+template <bool FP8, int ACT, bool RES, int XQ>
 static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
-    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES>;
+    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES, XQ>;
     static const int per_cu = resident_blocks(kern);
     // Persistent waves that all take the same number of tiles (to within
     // one): the fewest waves that keep the per-wave count of a full grid.
@@ -27,18 +27,26 @@ static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, st, a);
 }
 
-template <bool FP8, bool RES>
+template <bool FP8, bool RES, int XQ>
 static void launch_rows64_res(const RowsArgs& a, int act, hipStream_t st) {
-    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU, RES>(a, st);
-    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH, RES>(a, st);
-    else launch_rows64_act<FP8, ACT_NONE, RES>(a, st);
+    if (act == ACT_RELU) launch_rows64_act<FP8, ACT_RELU, RES, XQ>(a, st);
+    else if (act == ACT_GELU_TANH) launch_rows64_act<FP8, ACT_GELU_TANH, RES, XQ>(a, st);
+    else launch_rows64_act<FP8, ACT_NONE, RES, XQ>(a, st);
 }
 
-// a.residual (M x 64, 16-byte aligned) selects the FNO layer form act(x1 + x2).
+template <bool FP8, int XQ>
+static void launch_rows64_xq(const RowsArgs& a, int act, hipStream_t st) {
+    if (a.residual) launch_rows64_res<FP8, true, XQ>(a, act, st);
+    else launch_rows64_res<FP8, false, XQ>(a, act, st);
+}
+
+// a.residual (M x 64, 16-byte aligned) selects the FNO layer form act(x1 + x2),
+// a.xq_kind the x2 fake-quant.
 template <bool FP8>
 void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
-    if (a.residual) launch_rows64_res<FP8, true>(a, act, st);
-    else launch_rows64_res<FP8, false>(a, act, st);
+    if (a.xq_kind == 1) launch_rows64_xq<FP8, 1>(a, act, st);
+    else if (a.xq_kind == 2) launch_rows64_xq<FP8, 2>(a, act, st);
+    else launch_rows64_xq<FP8, 0>(a, act, st);
 }
 
 template void launch_rows64<false>(const RowsArgs&, int, hipStream_t);

@@ -125,7 +125,10 @@ __device__ __attribute__((noinline)) uint32_t pack4_token_scale(v4f v, float s) 
 }
 
 // RES: the FNO layer form act(x1 + x2) with x1 = a.residual (fno.cpp:650-654).
-template <bool FP8, int ACT, int PF = 1, bool RES = false>
+// XQ: the x2 fake-quant before it (fno.cpp:572-648): 1 per-tensor
+// (a.xq_scale, a.xq_zpf), 2 per-position (index column * a.xq_points +
+// row % a.xq_points into a.xq_scales / a.xq_zps).
+template <bool FP8, int ACT, int PF = 1, bool RES = false, int XQ = 0>
 __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     constexpr bool INT_EPI = !FP8;
     using L = Rows64Lds<FP8>;
@@ -212,6 +215,9 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         load_lin(tile + PF * nwaves, pre[PF - 1]);
         // Residual tile in the MFMA result layout: lane (r, g), column tile
         // nt -> row r, columns 16 nt + 4 g .. + 3.
+        // Position of row r for the per-position x2 fake-quant.
+        int xq_pos = 0;
+        if constexpr (XQ == 2) xq_pos = static_cast<int>((tile * 16 + r) % a.xq_points);
         v4f res[4];
         if constexpr (RES) {
             const auto rr = tile_rsrc(a.residual, tile * 16, M, 256);
@@ -383,7 +389,13 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             v4f y;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float x2 = dequant_bias(sw[v], s_r, t[v], bb[v]);
+                float x2 = dequant_bias(sw[v], s_r, t[v], bb[v]);
+                if constexpr (XQ == 1) {
+                    x2 = x2_fake_quant(x2, a.xq_scale, a.xq_zpf);
+                } else if constexpr (XQ == 2) {
+                    const int64_t idx = static_cast<int64_t>(16 * nt + 4 * g + v) * a.xq_points + xq_pos;
+                    x2 = x2_fake_quant(x2, a.xq_scales[idx], static_cast<float>(a.xq_zps[idx]));
+                }
                 if constexpr (RES) y[v] = activate<ACT>(res[nt][v] + x2);
                 else y[v] = activate<ACT>(x2);
             }

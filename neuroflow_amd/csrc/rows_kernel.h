@@ -84,6 +84,13 @@ struct RowsArgs {
     const float* residual;  // (M, N) or null: added before the activation (FNO layer)
     const int32_t* sum_in;     // IN_CODES: (M) row code sums, or null (the tiled GEMM only)
     const int32_t* colsum_in;  // (N) byte sums of W's rows over K, or null (the tiled GEMM only)
+    // x2 fake-quant of the FNO layer (nflow_x2_quant; k_rows64 and the FNO post-pass)
+    int xq_kind;               // 0 none, 1 per-tensor, 2 per-position
+    float xq_scale;
+    float xq_zpf;              // the zero point as float
+    const float* xq_scales;    // per-position: index j * xq_points + m % xq_points
+    const int32_t* xq_zps;
+    int xq_points;
 };
 
 // Operand dwords per lane per 64-wide K block: 16 int8 codes, or 16 bf16.

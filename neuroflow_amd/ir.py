@@ -117,6 +117,24 @@ class IR:
               "ir_fno_int8_dispatch")
         return (s.value, z.value) if use.value else None
 
+    def fno_x2_quant(self, layer_index: int, points: int = 0, device="cuda"):
+        """The x2 fake-quant of locs.{i} (fno.cpp:572-648) as a quant.X2Quant,
+        per-position arrays uploaded to `device`; None without one, and the
+        kind "fp8_log2" for the log2 snap (which the layers reject)."""
+        import torch
+        from .quant import X2Quant
+        q = _lib.X2QuantC()
+        check(_lib.lib().nflow_ir_fno_x2_quant(self._h, layer_index, C.byref(q)), "ir_fno_x2_quant")
+        if q.kind == _lib.X2_NONE:
+            return None
+        if q.kind == _lib.X2_PER_TENSOR:
+            return X2Quant("per_tensor", scale=q.scale, zero_point=q.zero_point)
+        if q.kind == _lib.X2_FP8_LOG2:
+            return X2Quant("fp8_log2", scale=q.scale)
+        s = torch.from_numpy(_arr(q.scales, q.n_positions, C.c_float)).to(device)
+        z = torch.from_numpy(_arr(q.zero_points, q.n_positions, C.c_int32)).to(device)
+        return X2Quant("per_position", scales=s, zero_points=z, width=q.width, points=points)
+
     def close(self) -> None:
         if self._h:
             _lib.lib().nflow_ir_close(self._h)

@@ -285,32 +285,70 @@ def fp8_linear_forward_per_token(p: Fp8LinearParams, A: torch.Tensor, activation
     return (out, s) if return_scales else out
 
 
-def _fno(fn_name, p, h, x1, activation, out, return_scales, what):
+@dataclass
+class X2Quant:
+    """The FNO layer's static INT8 fake-quant of x2 (fno.cpp:572-648),
+    nflow_x2_quant: "per_tensor" with (scale, zero_point), or "per_position"
+    with device arrays scales / zero_points of at least out_features * points
+    entries, indexed column * points + row % points (the reference's flat
+    (width, points) offset)."""
+
+    kind: str                                  # "per_tensor" | "per_position"
+    scale: float = 1.0
+    zero_point: int = 0
+    scales: Optional[torch.Tensor] = None      # (n_positions,) float32, device
+    zero_points: Optional[torch.Tensor] = None  # (n_positions,) int32, device
+    width: int = 0
+    points: int = 0
+
+    def c_struct(self) -> "_lib.X2QuantC":
+        kinds = {"none": _lib.X2_NONE, "per_tensor": _lib.X2_PER_TENSOR,
+                 "per_position": _lib.X2_PER_POSITION, "fp8_log2": _lib.X2_FP8_LOG2}
+        _dev(self.scales, torch.float32, "scales")
+        _dev(self.zero_points, torch.int32, "zero_points")
+        n = 0 if self.scales is None else self.scales.numel()
+        return _lib.X2QuantC(kinds[self.kind], float(self.scale), int(self.zero_point), _p(self.scales),
+                             _p(self.zero_points), n, int(self.width), int(self.points))
+
+
+def _fno(fn_name, p, h, x1, activation, out, return_scales, what, x2_quant=None):
     _dev(h, torch.float32, "h")
     _dev(x1, torch.float32, "x1")
     ps = p.c_struct()
     M = _rows(h, p.in_features)
-    if x1.shape[-1] != p.out_features or x1.numel() != M * p.out_features:
+    if x1 is not None and (x1.shape[-1] != p.out_features or x1.numel() != M * p.out_features):
         raise ValueError("x1 must be (M, out_features)")
     if out is None:
         out = torch.empty(*h.shape[:-1], p.out_features, dtype=torch.float32, device=h.device)
     s = torch.empty(M, dtype=torch.float32, device=h.device) if return_scales else None
-    check(getattr(_lib.lib(), fn_name)(C.byref(ps), M, _p(h), _p(x1), _p(out), _p(s), _act(activation),
-                                       _stream()), what)
+    if x2_quant is None:
+        if x1 is None:
+            raise ValueError("x1 is required without x2_quant")
+        check(getattr(_lib.lib(), fn_name)(C.byref(ps), M, _p(h), _p(x1), _p(out), _p(s), _act(activation),
+                                           _stream()), what)
+    else:
+        xq = x2_quant.c_struct()
+        check(getattr(_lib.lib(), fn_name + "_x2q")(C.byref(ps), M, _p(h), _p(x1), _p(out), _p(s),
+                                                    _act(activation), C.byref(xq), _stream()), what)
     return (out, s) if return_scales else out
 
 
-def fno_layer_per_token(p: Int8LinearParams, h: torch.Tensor, x1: torch.Tensor, activation="gelu",
-                        out: Optional[torch.Tensor] = None, return_scales: bool = False):
-    """The FNO local-linear layer act(x1 + (W q(h) + b)) with per-token INT8
-    (fno.cpp:515-557, 650-654); x1 is the spectral branch, (M, out_features)."""
-    return _fno("nflow_int8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fno_layer")
+def fno_layer_per_token(p: Int8LinearParams, h: torch.Tensor, x1: Optional[torch.Tensor], activation="gelu",
+                        out: Optional[torch.Tensor] = None, return_scales: bool = False,
+                        x2_quant: Optional[X2Quant] = None):
+    """The FNO local-linear layer act(x1 + fq(W q(h) + b)) with per-token INT8
+    (fno.cpp:515-557, 572-654); x1 is the spectral branch, (M, out_features),
+    and fq the optional x2 fake-quant."""
+    return _fno("nflow_int8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fno_layer",
+                x2_quant)
 
 
-def fp8_fno_layer_per_token(p: Fp8LinearParams, h: torch.Tensor, x1: torch.Tensor, activation="gelu",
-                            out: Optional[torch.Tensor] = None, return_scales: bool = False):
+def fp8_fno_layer_per_token(p: Fp8LinearParams, h: torch.Tensor, x1: Optional[torch.Tensor], activation="gelu",
+                            out: Optional[torch.Tensor] = None, return_scales: bool = False,
+                            x2_quant: Optional[X2Quant] = None):
     """fno_layer_per_token on the FP8 E4M3 path."""
-    return _fno("nflow_fp8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fp8_fno_layer")
+    return _fno("nflow_fp8_fno_layer_per_token", p, h, x1, activation, out, return_scales, "fp8_fno_layer",
+                x2_quant)
 
 
 def fp8_gemm_f32(A_q: torch.Tensor, W_q: torch.Tensor) -> torch.Tensor:
@@ -496,8 +534,10 @@ class Layer:
         return cls(_handle=h)
 
     def __call__(self, x: torch.Tensor, activation="gelu", out: Optional[torch.Tensor] = None,
-                 return_scales: bool = False, residual: Optional[torch.Tensor] = None):
-        """act(W q(x) + b), or with `residual` x1 the FNO form act(x1 + (W q(x) + b))."""
+                 return_scales: bool = False, residual: Optional[torch.Tensor] = None,
+                 x2_quant: Optional[X2Quant] = None):
+        """act(W q(x) + b), or with `residual` x1 the FNO form act(x1 + (W q(x) + b));
+        x2_quant adds the FNO layer's fake-quant of W q(x) + b."""
         _dev(x, torch.float32, "x")
         if x.shape[-1] != self.in_features:
             raise ValueError(f"x has {x.shape[-1]} features, the layer takes {self.in_features}")
@@ -506,7 +546,16 @@ class Layer:
             out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.float32, device=x.device)
         s = torch.empty(M, dtype=torch.float32, device=x.device) if return_scales else None
         sp = None if s is None else s.data_ptr()
-        if residual is None:
+        if x2_quant is not None:
+            if residual is not None:
+                _dev(residual, torch.float32, "residual")
+                if residual.numel() != M * self.out_features:
+                    raise ValueError("residual must be (M, out_features)")
+            xq = x2_quant.c_struct()
+            check(_lib.lib().nflow_layer_forward_fno(self._h, M, x.data_ptr(), _p(residual), out.data_ptr(), sp,
+                                                     _act(activation), C.byref(xq), _stream()),
+                  "layer_forward_fno")
+        elif residual is None:
             check(_lib.lib().nflow_layer_forward(self._h, M, x.data_ptr(), out.data_ptr(), sp,
                                                  _act(activation), _stream()), "layer_forward")
         else:

@@ -292,6 +292,51 @@ int orc_layer_per_token_i8(const orc_int8_linear_params* p, int64_t M,
     return ORC_OK;
 }
 
+/* fno.cpp:572-648, INT8 forms of the fake-quant of x2, on x2 held
+ * token-major (M = batch * points rows, N = width columns), as this library
+ * holds it.  The reference holds x2 as (batch, width, points) at that point
+ * (fno.cpp:550-556) and indexes it in its per-token loop (fno.cpp:615-633) as
+ * (batch, points, width); this restatement rebuilds the (batch, width,
+ * points) buffer, runs that loop as written, and maps back.  Per tensor
+ * (scales == NULL): every element with (scale, zp) (fno.cpp:634-646).
+ * M must be a multiple of points for the per-position form. */
+static float orc_fq1(float v, float scale, float zpf)
+{
+    float q = roundf(v / scale) + zpf;
+    if (q < -128.0f) q = -128.0f;
+    if (q > 127.0f) q = 127.0f;
+    return (q - zpf) * scale;
+}
+
+int orc_x2_fake_quant(const float* x2, float* out, int64_t M, int N, float scale, int32_t zp,
+                      const float* scales, const int32_t* zps, int points)
+{
+    if (!scales) {
+        const float zpf = (float)zp;
+        for (int64_t i = 0; i < M * (int64_t)N; ++i) out[i] = orc_fq1(x2[i], scale, zpf);
+        return ORC_OK;
+    }
+    if (points <= 0 || M % points != 0) return ORC_INVALID_ARG;
+    const int64_t n = points, w = N, bsz = M / points;
+    float* buf = (float*)malloc(sizeof(float) * (size_t)(n * w));
+    if (!buf) return ORC_INTERNAL;
+    for (int64_t bi = 0; bi < bsz; ++bi) {
+        /* x2 of sample bi as the reference holds it: [wi * n + ni]. */
+        for (int64_t wi = 0; wi < w; ++wi)
+            for (int64_t ni = 0; ni < n; ++ni) buf[wi * n + ni] = x2[(bi * n + ni) * w + wi];
+        /* fno.cpp:620-632: qp_idx = ni * w_axis + wi, off = ni * w_axis + wi. */
+        for (int64_t ni = 0; ni < n; ++ni)
+            for (int64_t wi = 0; wi < w; ++wi) {
+                const int64_t qp_idx = ni * w + wi;
+                buf[qp_idx] = orc_fq1(buf[qp_idx], scales[qp_idx], (float)zps[qp_idx]);
+            }
+        for (int64_t wi = 0; wi < w; ++wi)
+            for (int64_t ni = 0; ni < n; ++ni) out[(bi * n + ni) * w + wi] = buf[wi * n + ni];
+    }
+    free(buf);
+    return ORC_OK;
+}
+
 /* ---- FP8 E4M3 ---------------------------------------------------------- */
 
 /* fp8_e4m3.h:106-215.  The byte is assembled from the top three mantissa

@@ -100,6 +100,11 @@ int orc_linear_forward(const orc_int8_linear_params* p, const float* A,
 /* Epilogue activation, fno.cpp:36-48 (relu; gelu tanh form). */
 void orc_apply_activation(float* y, int64_t n, int act);
 
+/* fno.cpp:572-648: the FNO layer's INT8 fake-quant of x2 (token-major), per
+ * tensor (scales NULL) or per position (the reference's indexing). */
+int orc_x2_fake_quant(const float* x2, float* out, int64_t M, int N, float scale, int32_t zp,
+                      const float* scales, const int32_t* zps, int points);
+
 /* The per-token INT8 layer: for each row m, LinearForward with
  * scale_A = absmax(row)/127 (1.0f for a zero row), zp_A = 0, and the given
  * sum_W_per_row; then the activation.  scale_A_out (nullable) receives the

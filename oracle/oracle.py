@@ -79,6 +79,7 @@ def lib():
         L.orc_linear_forward_batched.argtypes = [C.POINTER(LinearParams), i64, vp, vp]
         L.orc_linear_forward.argtypes = [C.POINTER(LinearParams), vp, vp]
         L.orc_apply_activation.argtypes = [vp, i64, i32]
+        L.orc_x2_fake_quant.argtypes = [vp, vp, i64, i32, C.c_float, C.c_int32, vp, vp, i32]
         L.orc_layer_per_token_i8.argtypes = [C.POINTER(LinearParams), i64, vp, vp, i32, vp]
         L.orc_e4m3_encode.restype = C.c_uint8
         L.orc_e4m3_encode.argtypes = [f32]
@@ -195,6 +196,20 @@ def apply_activation(y, act):
     y = np.array(y, dtype=np.float32, copy=True, order="C")
     lib().orc_apply_activation(_ptr(y), y.size, act)
     return y
+
+
+def x2_fake_quant(x2, scale=1.0, zp=0, scales=None, zps=None, points=0):
+    """fno.cpp:572-648 on token-major x2 (M, N): per tensor, or per position
+    (scales / zps of N * points entries, the reference's indexing)."""
+    x2 = _f32(x2)
+    out = np.empty_like(x2)
+    sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+    zz = None if zps is None else np.ascontiguousarray(zps, np.int32)
+    rc = lib().orc_x2_fake_quant(_ptr(x2), _ptr(out), x2.shape[0], x2.shape[1], float(scale), int(zp),
+                                 None if sc is None else _ptr(sc), None if zz is None else _ptr(zz), int(points))
+    if rc != 0:
+        raise ValueError(f"orc_x2_fake_quant failed ({rc})")
+    return out
 
 
 def layer_per_token_i8(A, W_q, scale_W, zp_W=None, bias=None, sum_W=None, act=ACT_GELU_TANH):

@@ -87,3 +87,35 @@ def test_ir_layer_rejects_what_enable_int8_gemm_skips(gpu):
                      ("nope.weight", None), ("locs.0.weight", "nope.bias")]:
             with pytest.raises(NflowError):
                 ir.layer(*args)
+
+
+def test_ir_x2_fake_quant_drives_the_layer(gpu):
+    """IR.fno_x2_quant's precedence (FP8, per-token, per-tensor; fno.cpp:575-648)
+    and the per-position layer it feeds."""
+    rng = np.random.default_rng(8)
+    w, n = 64, 32
+    W = F.fno1d_weights(rng, 2, 1, w, 4, 3)
+    s, z = F.symmetric_per_channel(W["locs.0.weight"])
+    ps = rng.uniform(0.01, 0.05, n * w).astype(np.float32)
+    pz = rng.integers(-5, 5, n * w).astype(np.int32)
+    recs = [F.qparam_record(1, "locs.0.weight", s, z, 0),
+            F.qparam_record(2, "locs.0.output", ps, pz, w),
+            F.qparam_record(0, "locs.0.output", 0.5, 0),
+            F.qparam_record(0, "locs.1.output", 0.25, 3),
+            F.qparam_record(3, "locs.2.output", 0.125),
+            F.qparam_record(0, "locs.2.output", 0.5, 0)]
+    with IR(data=F.fno1d_file(W, [2, 1, w, 4, 3, 1, 0], recs)) as ir:
+        q0, q1, q2 = ir.fno_x2_quant(0, points=n), ir.fno_x2_quant(1), ir.fno_x2_quant(2)
+        assert q0.kind == "per_position" and q0.width == w
+        assert (q1.kind, q1.scale, q1.zero_point) == ("per_tensor", 0.25, 3)
+        assert q2.kind == "fp8_log2" and ir.fno_x2_quant(5) is None
+        layer = ir.layer("locs.0.weight", "locs.0.bias")
+        x = rng.normal(0, 1, (4 * n, w)).astype(np.float32)
+        x1 = rng.normal(0, 1, (4 * n, w)).astype(np.float32)
+        y = _host(layer(_cu(x), "relu", residual=_cu(x1), x2_quant=q0))
+        W_q, sum_W = O.quantise_weight_2d(W["locs.0.weight"], s, z)
+        x2, _ = O.layer_per_token_i8(x, W_q, s, z, W["locs.0.bias"], sum_W, O.ACT_NONE)
+        ref = O.apply_activation((x1 + O.x2_fake_quant(x2, scales=ps, zps=pz, points=n)).astype(np.float32),
+                                 O.ACT_RELU)
+        assert _same(y, ref)
+        layer.close()

@@ -10,6 +10,7 @@ from neuroflow_amd import workloads as WL
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-5, 1e-6
 
 
 def _cu(a):
@@ -113,3 +114,82 @@ def test_fno_layer_fp8_and_handle(gpu, M, N, K):
         assert _same(yl, O.apply_activation((_host(x1) + x2l).astype(np.float32), 1))
     with pytest.raises(Exception):
         Q.fno_layer_per_token(Q.Int8Linear(W, b).params, h, x1, "none", out=x1)
+
+
+# ---- the FNO layer's x2 fake-quant (fno.cpp:572-648) ------------------------
+
+def _x2q_params(kind, N, points, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "per_tensor":
+        return Q.X2Quant("per_tensor", scale=0.031, zero_point=-4), dict(scale=0.031, zp=-4)
+    s = rng.uniform(0.01, 0.08, N * points).astype(np.float32)
+    z = rng.integers(-10, 10, N * points).astype(np.int32)
+    return (Q.X2Quant("per_position", scales=_cu(s), zero_points=_cu(z), width=N, points=points),
+            dict(scales=s, zps=z, points=points))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 64, 64), (512, 256, 256), (256, 64, 100), (128, 1024, 1024)])
+@pytest.mark.parametrize("kind", ["per_tensor", "per_position"])
+@pytest.mark.parametrize("act,with_x1", [("relu", True), ("none", False), ("gelu", True)])
+def test_fno_layer_x2_fake_quant_int8(gpu, M, N, K, kind, act, with_x1):
+    points = 64
+    x = (WL.normal(60, (M, K)) * 2.0).astype(np.float32)
+    x1 = WL.normal(61, (M, N)).astype(np.float32) if with_x1 else None
+    W = WL.uniform(62, (N, K), -0.25, 0.25)
+    b = WL.uniform(63, (N,), -0.1, 0.1)
+    layer = Q.Int8Linear(W, b)
+    xq, oq = _x2q_params(kind, N, points, 64)
+    out = _host(Q.fno_layer_per_token(layer.params, _cu(x), None if x1 is None else _cu(x1), act, x2_quant=xq))
+    x2, _ = O.layer_per_token_i8(x, layer.W_q, layer.scale_W, None, b, layer.sum_W, O.ACT_NONE)
+    fq = O.x2_fake_quant(x2, **oq)
+    pre = fq if x1 is None else (x1 + fq).astype(np.float32)
+    ref = O.apply_activation(pre, {"none": 0, "relu": 1, "gelu": 2}[act])
+    if act == "gelu":
+        np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
+    else:
+        assert _same(out, ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 64, 64), (320, 256, 256)])
+@pytest.mark.parametrize("kind", ["per_tensor", "per_position"])
+def test_fno_layer_x2_fake_quant_fp8(gpu, M, N, K, kind):
+    """FP8 x2 agrees with the exact-product oracle to 1e-5 / 1e-6, so a fake-quant
+    step can flip where x2 sits at a rounding boundary: outputs equal the
+    oracle's up to one quantisation step, and almost all exactly."""
+    points = 32
+    x = (2.0 * WL.normal(65, (M, K))).astype(np.float32)
+    x1 = WL.normal(66, (M, N)).astype(np.float32)
+    W = WL.uniform(67, (N, K), -0.125, 0.125)
+    b = WL.uniform(68, (N,), -0.1, 0.1)
+    layer = Q.Fp8Linear(W, b)
+    xq, oq = _x2q_params(kind, N, points, 69)
+    out = _host(Q.fp8_fno_layer_per_token(layer.params, _cu(x), _cu(x1), "relu", x2_quant=xq))
+    qa, sa = O.quantise_per_token_fp8(x)
+    x2 = O.layer_fp8_exact(qa, sa, layer.W_q, layer.scale_W, b, O.ACT_NONE)
+    ref = O.apply_activation((x1 + O.x2_fake_quant(x2, **oq)).astype(np.float32), O.ACT_RELU)
+    step = oq["scale"] if kind == "per_tensor" else float(oq["scales"].max())
+    assert np.all(np.abs(out - ref) <= step * 1.001 + 1e-5)
+    assert np.mean(out != ref) < 0.01
+
+
+def test_fno_layer_x2_fake_quant_on_handles_and_errors(gpu):
+    from neuroflow_amd._lib import NflowError, SHAPE_MISMATCH, UNSUPPORTED_OP
+    M, N, K = 1024, 64, 64
+    x = WL.normal(70, (M, K)).astype(np.float32)
+    x1 = WL.normal(71, (M, N)).astype(np.float32)
+    W = WL.uniform(72, (N, K), -0.25, 0.25)
+    b = WL.uniform(73, (N,), -0.1, 0.1)
+    h = Q.Layer(W, b, fmt="int8")
+    p = Q.Int8Linear(W, b)
+    xq, _ = _x2q_params("per_position", N, 16, 74)
+    y_h = _host(h(_cu(x), "relu", residual=_cu(x1), x2_quant=xq))
+    y_p = _host(Q.fno_layer_per_token(p.params, _cu(x), _cu(x1), "relu", x2_quant=xq))
+    assert _same(y_h, y_p)
+    bad = [Q.X2Quant("fp8_log2", scale=0.5),
+           Q.X2Quant("per_position", scales=xq.scales, zero_points=xq.zero_points, width=N + 1, points=16),
+           Q.X2Quant("per_position", scales=xq.scales, zero_points=xq.zero_points, width=N, points=17)]
+    for q, code in zip(bad, [UNSUPPORTED_OP, SHAPE_MISMATCH, SHAPE_MISMATCH]):
+        with pytest.raises(NflowError) as e:
+            h(_cu(x), "relu", residual=_cu(x1), x2_quant=q)
+        assert e.value.code == code
+    h.close()
