@@ -161,6 +161,30 @@ void orc_layer_fp8_exact(const uint8_t* A_q, const float* scale_A,
                          const float* bias, int64_t M, int N, int K, int act,
                          float* C);
 
+
+/* ---- FNO1d forward pieces (nflow_oracle_fno.c) --------------------------- */
+
+/* fft.cpp:48-68: in-place complex FFT of n (a power of two) interleaved
+ * complex values; inverse != 0 runs the inverse with the 1/n scaling. */
+void orc_cfft(float* a, int n, int inverse);
+/* fft.cpp:72-84 / :86-100. */
+void orc_rfft(const float* x, int n, float* out_complex);
+void orc_irfft(const float* x_complex, int n, float* out);
+/* fno.cpp:164-207: h, out (bsz, w, n); w_real / w_imag (w, w, modes). */
+void orc_spectral_conv1d(const float* h, int bsz, int w, int n, int modes,
+                         const float* w_real, const float* w_imag, float* out);
+/* fno.cpp:69-79: y (rows, n) = b + x (rows, k) @ W^T, summed in order the way the
+ * reference build does (blocks of 16 / 8 rounded products, fused tail). */
+void orc_linear_f32(const float* x, const float* W, const float* b, int64_t rows, int k, int n,
+                    float* y);
+/* The INT8 fake-quant round trip with one (scale, zero point) per element. */
+void orc_fake_quant_arr(const float* in, const float* scales, const int32_t* zps, float* out,
+                        int64_t n);
+/* fno.cpp:579-606: the log2 "FP8" snap of x2 (per-tensor scale s). */
+float orc_log2_snap_one(float x, float s);
+void orc_log2_snap(const float* in, float s, float* out, int64_t n);
+int orc_log2_snap_exponent(float a);
+
 #ifdef __cplusplus
 }
 #endif

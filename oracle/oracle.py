@@ -97,6 +97,17 @@ def lib():
         L.orc_gemm_fp8_exact.argtypes = [vp, vp, i64, i32, i32, vp]
         L.orc_layer_fp8_composed.argtypes = [vp, vp, vp, i64, i32, i32, i32, vp, vp, vp]
         L.orc_layer_fp8_exact.argtypes = [vp, vp, vp, vp, vp, i64, i32, i32, i32, vp]
+        L.orc_cfft.argtypes = [vp, i32, i32]
+        L.orc_rfft.argtypes = [vp, i32, vp]
+        L.orc_irfft.argtypes = [vp, i32, vp]
+        L.orc_spectral_conv1d.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp]
+        L.orc_linear_f32.argtypes = [vp, vp, vp, i64, i32, i32, vp]
+        L.orc_fake_quant_arr.argtypes = [vp, vp, vp, vp, i64]
+        L.orc_log2_snap_one.restype = f32
+        L.orc_log2_snap_one.argtypes = [f32, f32]
+        L.orc_log2_snap.argtypes = [vp, f32, vp, i64]
+        L.orc_log2_snap_exponent.restype = i32
+        L.orc_log2_snap_exponent.argtypes = [f32]
     return _lib
 
 
@@ -225,6 +236,67 @@ def layer_per_token_i8(A, W_q, scale_W, zp_W=None, bias=None, sum_W=None, act=AC
     assert rc == 0, rc
     del keep
     return out, sa
+
+
+# ---- FNO1d forward pieces -----------------------------------------------------
+
+def rfft(x):
+    """fft.cpp:72-84 on a 1-D float32 array of power-of-two length."""
+    x = _f32(x)
+    out = np.empty(2 * (x.size // 2 + 1), np.float32)
+    lib().orc_rfft(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def irfft(xc, n):
+    """fft.cpp:86-100: n/2 + 1 interleaved bins -> n reals."""
+    xc = _f32(xc)
+    assert xc.size == 2 * (n // 2 + 1)
+    out = np.empty(n, np.float32)
+    lib().orc_irfft(_ptr(xc), n, _ptr(out))
+    return out
+
+
+def spectral_conv1d(h, w_real, w_imag, modes):
+    """fno.cpp:164-207: h (b, w, n) -> (b, w, n)."""
+    h = _f32(h)
+    b, w, n = h.shape
+    wr, wi = _f32(w_real), _f32(w_imag)
+    assert wr.shape == (w, w, modes) and wi.shape == wr.shape
+    out = np.empty_like(h)
+    lib().orc_spectral_conv1d(_ptr(h), b, w, n, modes, _ptr(wr), _ptr(wi), _ptr(out))
+    return out
+
+
+def linear_f32(x, W, b=None):
+    """fno.cpp:69-79: x (rows, k) -> (rows, n), bias first, sequential over k."""
+    x = _f32(x)
+    W = _f32(W)
+    bb = None if b is None else _f32(b)
+    rows, k = x.shape
+    n = W.shape[0]
+    assert W.shape[1] == k
+    y = np.empty((rows, n), np.float32)
+    lib().orc_linear_f32(_ptr(x), _ptr(W), None if bb is None else _ptr(bb), rows, k, n, _ptr(y))
+    return y
+
+
+def fake_quant_elementwise(x, scales, zps):
+    """The INT8 fake-quant round trip with per-element (broadcast) scales / zero points."""
+    x = _f32(x)
+    s = np.ascontiguousarray(np.broadcast_to(np.asarray(scales, np.float32), x.shape))
+    z = np.ascontiguousarray(np.broadcast_to(np.asarray(zps, np.int32), x.shape))
+    out = np.empty_like(x)
+    lib().orc_fake_quant_arr(_ptr(x), _ptr(s), _ptr(z), _ptr(out), x.size)
+    return out
+
+
+def log2_snap(x, scale):
+    """fno.cpp:579-606 (the log2 "FP8" snap of x2, per-tensor scale)."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_log2_snap(_ptr(x), float(scale), _ptr(out), x.size)
+    return out
 
 
 # ---- FP8 --------------------------------------------------------------------
