@@ -1,4 +1,4 @@
-"""ctypes binding of libnflow_quant.so (include/nflow_quant.h).
+"""ctypes binding of libnflow_quant.so (include/nflow_quant.h, include/nflow_runtime.h).
 
 The library is loaded from neuroflow_amd/lib/ (built in-tree by
 `python -m neuroflow_amd.build`).  There is no fallback: if the library is
@@ -129,8 +129,19 @@ SIGNATURES = {
     "nflow_ir_layer_create": [_vp, C.c_char_p, C.c_char_p, C.POINTER(_vp)],
     "nflow_ir_fno_int8_dispatch": [_vp, _i32, C.POINTER(_i32), C.POINTER(C.c_float), C.POINTER(C.c_int32)],
     "nflow_ir_fno_x2_quant": [_vp, _i32, C.POINTER(X2QuantC)],
+    # include/nflow_runtime.h
+    "nflow_runtime_create": [C.c_char_p, C.POINTER(_vp)],
+    "nflow_runtime_create_memory": [_vp, C.c_size_t, C.POINTER(_vp)],
+    "nflow_runtime_destroy": [_vp],
+    "nflow_runtime_op": [_vp],
+    "nflow_runtime_config": [_vp, C.POINTER(C.c_int32), C.POINTER(_i32), C.POINTER(_i32)],
+    "nflow_runtime_enable_int8_gemm": [_vp],
+    "nflow_runtime_is_int8_gemm_enabled": [_vp, C.POINTER(_i32)],
+    "nflow_runtime_layer_dispatch": [_vp, _i32, C.POINTER(_i32)],
+    "nflow_runtime_run": [_vp, _vp, C.POINTER(C.c_int64), _i32, _vp, C.POINTER(C.c_int64), _i32],
+    "nflow_runtime_run_device": [_vp, _vp, C.POINTER(C.c_int64), _i32, _vp, C.POINTER(C.c_int64), _i32, _vp],
 }
-_RESTYPES = {"nflow_last_error": C.c_char_p}
+_RESTYPES = {"nflow_last_error": C.c_char_p, "nflow_runtime_op": C.c_char_p}
 
 _lib = None
 

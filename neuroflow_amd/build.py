@@ -1,9 +1,13 @@
-"""Build libnflow_quant.so (the gfx950 kernels + C-ABI) in-tree.
+"""Build libnflow_quant.so (the gfx950 kernels + C-ABI) in-tree, and the
+pybind11 module neuroflow_cpp on top of it.
 
     python -m neuroflow_amd.build
 
 Compiles neuroflow_amd/csrc/*.hip and *.cpp with hipcc for gfx950 and links
-neuroflow_amd/lib/libnflow_quant.so.  Flags:
+neuroflow_amd/lib/libnflow_quant.so; then compiles
+neuroflow_amd/bindings/neuroflow_cpp.cpp (host code only) into
+neuroflow_amd/lib/neuroflow_cpp<ext>, which loads the library from its own
+directory.  Flags:
   -ffp-contract=off   float expressions round in the written order (the
                       dequantise step must match the reference bit for bit);
   -target-feature -packed-fp32-ops   no packed fp32 VALU instructions.
@@ -45,6 +49,30 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
+def build_bindings(verbose: bool = True) -> Path:
+    """neuroflow_cpp: g++ against pybind11 and the Python headers, linked to
+    libnflow_quant.so with an $ORIGIN rpath."""
+    import sysconfig
+
+    import pybind11
+
+    out = LIB_DIR / ("neuroflow_cpp" + sysconfig.get_config_var("EXT_SUFFIX"))
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-D__HIP_PLATFORM_AMD__",
+           "-I", str(PKG.parent / "include"), "-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"],
+           "-I", str(rocm / "include"), str(PKG / "bindings" / "neuroflow_cpp.cpp"), "-o", str(tmp),
+           "-L", str(LIB_DIR), "-lnflow_quant", "-Wl,-rpath,$ORIGIN", "-L", str(rocm / "lib"), "-lamdhip64",
+           "-Wl,-rpath," + str(rocm / "lib")]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"bindings build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def build(verbose: bool = True, lib: Path = LIB) -> Path:
     srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     obj_dir = PKG / "_build" / lib.stem
@@ -67,5 +95,9 @@ def build(verbose: bool = True, lib: Path = LIB) -> Path:
 
 
 if __name__ == "__main__":
-    build(lib=Path(sys.argv[1]).resolve() if len(sys.argv) > 1 else LIB)
+    if len(sys.argv) > 1:
+        build(lib=Path(sys.argv[1]).resolve())
+    else:
+        build()
+        build_bindings()
     sys.exit(0)

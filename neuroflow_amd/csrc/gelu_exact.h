@@ -1,0 +1,151 @@
+// gelu_exact.h -- the reference's GELU bit for bit.
+//
+// fno.cpp:41-46 evaluates 0.5f * z * (1 + std::tanh(c * (z + 0.044715f z^3)))
+// with glibc's tanhf; its build (g++ -O3 -mfma) fuses the last product of the
+// cubic term with the addition.  glibc's float tanhf and expm1f are the
+// fdlibm algorithms (Sun Microsystems, freely distributable): tanhf from
+// expm1f of 2|x|, expm1f by argument reduction x = k ln2 + r and a rational
+// approximation in r^2 with the published coefficients below.  This
+// restatement reproduces glibc 2.35's tanhf on every one of the 2^32 float
+// inputs when each float operation is rounded on its own (-ffp-contract=off,
+// correctly rounded division), which both the host build and the gfx950
+// build of this library do.
+//
+// Usable from host code (the test harness) and device code.
+#pragma once
+
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIP__)
+#define NFQ_HD __host__ __device__
+#else
+#define NFQ_HD
+#endif
+
+namespace nfq {
+
+NFQ_HD inline uint32_t gx_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    return u;
+}
+NFQ_HD inline float gx_float(uint32_t u) {
+    float x;
+    memcpy(&x, &u, 4);
+    return x;
+}
+NFQ_HD inline float gx_fabs(float x) { return gx_float(gx_bits(x) & 0x7fffffffu); }
+
+// fdlibm expm1f: e^x - 1.
+NFQ_HD inline float expm1f_fdlibm(float x) {
+    const float o_threshold = 8.8721679688e+01f, ln2_hi = 6.9313812256e-01f,
+                ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
+                Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+    float hi, lo, c = 0.0f, t;
+    int32_t k;
+    uint32_t hx = gx_bits(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {                 // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {             // |x| >= 88.72...
+            if (hx > 0x7f800000u) return x + x;                  // NaN
+            if (hx == 0x7f800000u) return xsb == 0 ? x : -1.0f;  // +-Inf
+            if (x > o_threshold) return gx_float(0x7f800000u);  // overflow
+        }
+        if (xsb != 0) return -1.0f;          // x < -27 ln2
+    }
+    if (hx > 0x3eb17218u) {                  // |x| > 0.5 ln2
+        if (hx < 0x3F851592u) {              // and < 1.5 ln2
+            if (xsb == 0) {
+                hi = x - ln2_hi;
+                lo = ln2_lo;
+                k = 1;
+            } else {
+                hi = x + ln2_hi;
+                lo = -ln2_lo;
+                k = -1;
+            }
+        } else {
+            k = static_cast<int32_t>(invln2 * x + ((xsb == 0) ? 0.5f : -0.5f));
+            t = static_cast<float>(k);
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) {           // |x| < 2^-25
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x;
+    const float hxs = x * hfx;
+    const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    t = 3.0f - r1 * hfx;
+    float e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    const float twopk = gx_float(0x3f800000u + (static_cast<uint32_t>(k) << 23));
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return 1.0f + 2.0f * (x - e);
+    }
+    float y;
+    if (k <= -2 || k > 56) {
+        y = 1.0f - (e - x);
+        if (k == 128)
+            y = y * 2.0f * gx_float(0x7f000000u);
+        else
+            y = y * twopk;
+        return y - 1.0f;
+    }
+    if (k < 23) {
+        t = gx_float(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+        y = t - (e - x);
+        y = y * twopk;
+    } else {
+        t = gx_float(static_cast<uint32_t>(0x7f - k) << 23);  // 2^-k
+        y = x - (e + t);
+        y += 1.0f;
+        y = y * twopk;
+    }
+    return y;
+}
+
+// fdlibm tanhf.
+NFQ_HD inline float tanhf_fdlibm(float x) {
+    const uint32_t jx = gx_bits(x), ix = jx & 0x7fffffffu;
+    float z;
+    if (ix >= 0x7f800000u) {                 // Inf or NaN
+        return (jx & 0x80000000u) == 0 ? 1.0f / x + 1.0f : 1.0f / x - 1.0f;
+    }
+    if (ix < 0x41b00000u) {                  // |x| < 22
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return x * (1.0f + x);  // |x| < 2^-55
+        if (ix >= 0x3f800000u) {             // |x| >= 1
+            const float t = expm1f_fdlibm(2.0f * gx_fabs(x));
+            z = 1.0f - 2.0f / (t + 2.0f);
+        } else {
+            const float t = expm1f_fdlibm(-2.0f * gx_fabs(x));
+            z = -t / (t + 2.0f);
+        }
+    } else {
+        z = 1.0f;                            // 1 - tiny rounds to 1
+    }
+    return (jx & 0x80000000u) == 0 ? z : -z;
+}
+
+// c = std::sqrt(2.0f / static_cast<float>(M_PI)) (fno.cpp:42).
+constexpr float kGeluC = 0x1.988452p-1f;
+
+// fno.cpp:41-46 as the reference build computes it.
+NFQ_HD inline float gelu_ref(float z) {
+    const float inner = __builtin_fmaf((0.044715f * z) * z, z, z);
+    return (0.5f * z) * (1.0f + tanhf_fdlibm(kGeluC * inner));
+}
+
+}  // namespace nfq

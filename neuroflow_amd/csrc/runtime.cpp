@@ -1,0 +1,647 @@
+// runtime.cpp -- nflow::InferenceRuntime for FNO1d on the device
+// (cpp/src/runtime.cpp:15-101, 150-173, cpp/include/neuroflow/runtime.h:
+// 64-121): load a NeuroIR binary, apply the NIRQ weight fake-quant
+// (fno.cpp:209-300), optionally build the INT8 local-linear blobs
+// (EnableInt8Gemm, fno.cpp:325-406), and run FNO1d::Forward (fno.cpp:
+// 408-700) with every stage on the GPU:
+//   lift (fp32 Linear) -> L x [input fake-quant, spectral convolution,
+//   local linear (INT8 LinearForwardBatched when dispatched, fp32 Linear
+//   otherwise), act(x1 + fq(x2))] -> proj_q + act -> proj_out.
+// The weights live in HBM from creation on; a run allocates nothing once
+// its workspace (grown on demand) fits the shape.
+#include <hip/hip_runtime_api.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "fno1d.h"
+#include "nflow_quant.h"
+#include "nflow_runtime.h"
+#include "status.h"
+
+namespace nfq {
+namespace {
+
+struct LayerQuant {
+    bool in_fq = false;       // fake-quant of the layer input (fno.cpp:488-501)
+    float in_scale = 1.0f;
+    int32_t in_zp = 0;
+    int x2_kind = 0;          // 0 none, 1 per tensor, 2 per position, 3 log2 snap
+    float x2_scale = 1.0f;
+    int32_t x2_zp = 0;
+    int pos_width = 0;        // per position: the qparam's width
+    int64_t pos_count = 0;    // and its number of entries
+    size_t pos_off = 0;       // offset of its scales / zero points in the weight block
+    bool int8 = false;        // LinearDispatchTryInt8 takes the INT8 path (fno.cpp:125-159)
+    float sa = 1.0f;
+    int32_t zpa = 0;
+};
+
+void host_fake_quant(float* v, size_t n, float s, float zpf) {
+    // fno.cpp:250-255.
+    for (size_t i = 0; i < n; ++i) {
+        float q = std::round(v[i] / s) + zpf;
+        if (q < -128.0f) q = -128.0f;
+        if (q > 127.0f) q = 127.0f;
+        v[i] = (q - zpf) * s;
+    }
+}
+
+int snap_exponent_host(float a) {
+    const float r = std::round(std::log2(a) * 8.0f) / 8.0f;
+    return (r >= -2147483648.0f && r < 2147483648.0f) ? static_cast<int>(r) : INT_MIN;
+}
+
+uint32_t fbits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+float ffrom(uint32_t u) {
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// The exponent steps of the log2 snap (fno.cpp:594-601) under this host's
+// libm, which is the reference's: the exponent int(round(8 log2 a) / 8) goes
+// from -6 (a = 2^-6) to 9 in 15 steps, at a = 2^(-m + 1/16) (m = 6 .. 1) and
+// a = 2^(m - 1/16) (m = 1 .. 9).  Each step point is located exactly by
+// scanning the floats around it; the scan also checks that the exponent is
+// monotone there.
+bool snap_thresholds(float thr[15]) {
+    int j = 0;
+    for (int m = -6; m <= 8; ++m) {
+        const int after = m + 1;
+        const double target = after <= 0 ? std::exp2(after - 1 + 1.0 / 16) : std::exp2(after - 1.0 / 16);
+        const uint32_t u0 = fbits(static_cast<float>(target));
+        uint32_t first = 0;
+        int prev = INT_MIN;
+        for (uint32_t u = u0 - 512; u <= u0 + 512; ++u) {
+            const int e = snap_exponent_host(ffrom(u));
+            if (e != m && e != after) return false;
+            if (prev != INT_MIN && e < prev) return false;
+            if (e == after && !first) first = u;
+            prev = e;
+        }
+        if (!first || snap_exponent_host(ffrom(u0 - 512)) != m) return false;
+        thr[j++] = ffrom(first);
+    }
+    return true;
+}
+
+// Stage twiddles of fft.cpp:50-63 (w starts at (1, 0), w *= wlen with
+// wlen = (cos, sin) of (+-2 * pi) / len; the product in the reference
+// build's fused form), stage len at entries len/2 - 1 .. len - 2.
+void twiddles(int n, bool inverse, std::vector<float>& out) {
+    out.assign(2 * static_cast<size_t>(n > 1 ? n - 1 : 1), 0.0f);
+    for (int len = 2; len <= n; len <<= 1) {
+        const float ang = (inverse ? 2.0f : -2.0f) * static_cast<float>(M_PI) / static_cast<float>(len);
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        float wr = 1.0f, wi = 0.0f;
+        const int half = len / 2;
+        for (int k = 0; k < half; ++k) {
+            out[2 * static_cast<size_t>(half - 1 + k)] = wr;
+            out[2 * static_cast<size_t>(half - 1 + k) + 1] = wi;
+            const float nr = std::fma(wr, cs, -(wi * sn));
+            const float ni = std::fma(wr, sn, wi * cs);
+            wr = nr;
+            wi = ni;
+        }
+    }
+}
+
+bool is_pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
+
+}  // namespace
+}  // namespace nfq
+
+using namespace nfq;
+
+struct nflow_runtime {
+    std::string op;
+    int device = 0;
+    int in_ch = 0, out_ch = 0, width = 0, modes = 0, n_layers = 0, pad_factor = 1;
+    int act = RT_ACT_GELU;
+    bool quant_enabled = false;
+    bool int8_enabled = false;
+
+    // Host copies of the IR data the runtime needs after creation.
+    nflow_ir* ir = nullptr;
+    std::map<std::string, std::vector<float>> w;   // weights after the NIRQ fake-quant
+    std::vector<LayerQuant> lq;
+    float thr[15] = {};
+
+    // Device: one block for every fp32 weight and per-position qparam.
+    void* dblock = nullptr;
+    std::map<std::string, size_t> off;  // float offsets into dblock
+    std::vector<nflow_layer*> int8_layers;
+
+    // Device twiddles per grid length, workspace grown on demand.
+    std::map<int, float*> tw;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+
+    const float* dw(const std::string& name) const {
+        return static_cast<const float*>(dblock) + off.at(name);
+    }
+};
+
+namespace nfq {
+namespace {
+
+void free_runtime(nflow_runtime* rt) {
+    if (!rt) return;
+    int cur = 0;
+    const bool sw = hipGetDevice(&cur) == hipSuccess && cur != rt->device;
+    if (sw) (void)hipSetDevice(rt->device);
+    for (auto* l : rt->int8_layers) nflow_layer_destroy(l);
+    for (auto& kv : rt->tw) (void)hipFree(kv.second);
+    if (rt->dblock) (void)hipFree(rt->dblock);
+    if (rt->ws) (void)hipFree(rt->ws);
+    if (sw) (void)hipSetDevice(cur);
+    if (rt->ir) nflow_ir_close(rt->ir);
+    delete rt;
+}
+
+int parse_err(const std::string& m) { return set_error(NFLOW_PARSE_ERROR, "runtime: " + m); }
+
+// The weight of the fixed FNO1d sequence (ir_loader.h:274-298) with the
+// shape the configuration implies.
+int take_weight(nflow_runtime* rt, const std::string& name, std::vector<int64_t> dims) {
+    int ndim = 0;
+    int64_t d8[8] = {};
+    const float* data = nullptr;
+    if (nflow_ir_weight(rt->ir, name.c_str(), &ndim, d8, &data) != NFLOW_OK)
+        return parse_err("weight name mismatch: " + name + " is missing");
+    if (ndim != static_cast<int>(dims.size()))
+        return parse_err("weight " + name + " has the wrong rank for the configuration");
+    int64_t numel = 1;
+    for (int i = 0; i < ndim; ++i) {
+        if (d8[i] != dims[i]) return parse_err("weight " + name + " has the wrong shape for the configuration");
+        numel *= d8[i];
+    }
+    rt->w[name].assign(data, data + numel);
+    return NFLOW_OK;
+}
+
+// EnablePerChannelWeightDequant (fno.cpp:209-300): per-channel qparams of a
+// 2-D weight on axis 0 or a 3-D spectral weight on axis 1, else the weight's
+// per-tensor qparam.
+int dequantise_weight(nflow_runtime* rt, const std::string& name) {
+    std::vector<float>& t = rt->w[name];
+    int found = 0, n_ch = 0, axis = 0, ndim = 0;
+    int64_t d8[8] = {};
+    const float* sc = nullptr;
+    const int32_t* zp = nullptr;
+    (void)nflow_ir_weight(rt->ir, name.c_str(), &ndim, d8, nullptr);
+    (void)nflow_ir_per_channel_qparam(rt->ir, name.c_str(), &found, &n_ch, &axis, &sc, &zp);
+    if (found) {
+        if (ndim == 2 && axis == 0) {
+            if (n_ch > d8[0]) return set_error(NFLOW_SHAPE_MISMATCH, "runtime: more channel qparams than rows of " + name);
+            for (int64_t c = 0; c < n_ch; ++c)
+                host_fake_quant(t.data() + c * d8[1], static_cast<size_t>(d8[1]), sc[c], static_cast<float>(zp[c]));
+            return NFLOW_OK;
+        }
+        if (ndim == 3 && axis == 1) {
+            if (n_ch < d8[1]) return set_error(NFLOW_SHAPE_MISMATCH, "runtime: fewer channel qparams than channels of " + name);
+            for (int64_t i = 0; i < d8[0]; ++i)
+                for (int64_t c = 0; c < d8[1]; ++c)
+                    host_fake_quant(t.data() + (i * d8[1] + c) * d8[2], static_cast<size_t>(d8[2]), sc[c],
+                                    static_cast<float>(zp[c]));
+            return NFLOW_OK;
+        }
+    }
+    float s = 1.0f;
+    int32_t z = 0;
+    (void)nflow_ir_per_tensor_qparam(rt->ir, name.c_str(), &found, &s, &z);
+    if (found) host_fake_quant(t.data(), t.size(), s, static_cast<float>(z));
+    return NFLOW_OK;
+}
+
+std::vector<std::string> weight_names(const nflow_runtime* rt) {
+    std::vector<std::string> names = {"lift.weight", "lift.bias"};
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const std::string p = "specs." + std::to_string(i);
+        names.push_back(p + ".weights_real");
+        names.push_back(p + ".weights_imag");
+    }
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const std::string p = "locs." + std::to_string(i);
+        names.push_back(p + ".weight");
+        names.push_back(p + ".bias");
+    }
+    for (const char* s : {"proj_q.weight", "proj_q.bias", "proj_out.weight", "proj_out.bias"}) names.push_back(s);
+    return names;
+}
+
+int init(nflow_runtime* rt) {
+    int version = 0, op = 0, act = 0, quant = 0;
+    int32_t cfg[8] = {};
+    if (int rc = nflow_ir_header(rt->ir, &version, &op, cfg, &act, &quant)) return rc;
+    static const char* kOps[] = {"", "FNO1d", "FNO2d", "FNO3d", "DeepONet", "TokenMixer", "GraphOp",
+                                 "TokenMixer2D", "GraphOp2D"};
+    rt->op = (op >= 1 && op <= 8) ? kOps[op] : "";
+    if (op != 1)
+        return set_error(NFLOW_UNSUPPORTED_OP,
+                         "runtime: the device runtime serves FNO1d (the op with the quantised "
+                         "local-linear path); this IR holds " + rt->op);
+    rt->in_ch = cfg[0];
+    rt->out_ch = cfg[1];
+    rt->width = cfg[2];
+    rt->modes = cfg[3];
+    rt->n_layers = cfg[4];
+    rt->pad_factor = cfg[5];
+    rt->act = act == 1 ? RT_ACT_RELU : RT_ACT_GELU;
+    rt->quant_enabled = quant != 0;
+    if (rt->in_ch <= 0 || rt->out_ch <= 0 || rt->width <= 0 || rt->modes < 0 || rt->n_layers < 0)
+        return parse_err("bad FNO1d configuration");
+    const int64_t w = rt->width, m = rt->modes;
+    if (int rc = take_weight(rt, "lift.weight", {w, rt->in_ch})) return rc;
+    if (int rc = take_weight(rt, "lift.bias", {w})) return rc;
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const std::string s = "specs." + std::to_string(i), l = "locs." + std::to_string(i);
+        if (int rc = take_weight(rt, s + ".weights_real", {w, w, m})) return rc;
+        if (int rc = take_weight(rt, s + ".weights_imag", {w, w, m})) return rc;
+        if (int rc = take_weight(rt, l + ".weight", {w, w})) return rc;
+        if (int rc = take_weight(rt, l + ".bias", {w})) return rc;
+    }
+    if (int rc = take_weight(rt, "proj_q.weight", {w, w})) return rc;
+    if (int rc = take_weight(rt, "proj_q.bias", {w})) return rc;
+    if (int rc = take_weight(rt, "proj_out.weight", {rt->out_ch, w})) return rc;
+    if (int rc = take_weight(rt, "proj_out.bias", {rt->out_ch})) return rc;
+    if (rt->quant_enabled)
+        for (const auto& name : weight_names(rt))
+            if (int rc = dequantise_weight(rt, name)) return rc;
+
+    // Per-layer activation quantisation (fno.cpp:482-501, 571-648).
+    rt->lq.assign(rt->n_layers, LayerQuant{});
+    bool any_snap = false;
+    std::vector<std::pair<std::vector<float>, std::vector<int32_t>>> pos(rt->n_layers);
+    for (int i = 0; i < rt->n_layers && rt->quant_enabled; ++i) {
+        LayerQuant& q = rt->lq[i];
+        const std::string in_key = i == 0 ? "lift.output" : "locs." + std::to_string(i - 1) + ".output";
+        int found = 0;
+        (void)nflow_ir_per_tensor_qparam(rt->ir, in_key.c_str(), &found, &q.in_scale, &q.in_zp);
+        q.in_fq = found != 0;
+        const std::string key = "locs." + std::to_string(i) + ".output";
+        float fs = 0.0f;
+        (void)nflow_ir_fp8_qparam(rt->ir, key.c_str(), &found, &fs);
+        if (found) {
+            if (fs > 0.0f) {
+                q.x2_kind = 3;
+                q.x2_scale = fs;
+                any_snap = true;
+            }
+            continue;
+        }
+        int n_tok = 0, width = 0;
+        const float* ps = nullptr;
+        const int32_t* pz = nullptr;
+        (void)nflow_ir_per_token_qparam(rt->ir, key.c_str(), &found, &n_tok, &width, &ps, &pz);
+        if (found) {
+            q.x2_kind = 2;
+            q.pos_width = width;
+            q.pos_count = n_tok;
+            pos[i].first.assign(ps, ps + n_tok);
+            pos[i].second.assign(pz, pz + n_tok);
+            continue;
+        }
+        (void)nflow_ir_per_tensor_qparam(rt->ir, key.c_str(), &found, &q.x2_scale, &q.x2_zp);
+        if (found) q.x2_kind = 1;
+    }
+    if (any_snap && !snap_thresholds(rt->thr))
+        return set_error(NFLOW_INTERNAL, "runtime: the host libm's log2 is not monotone at a snap step");
+
+    // Upload: every weight, then the per-position qparams (scales, then zps).
+    size_t total = 0;
+    for (const auto& kv : rt->w) {
+        rt->off[kv.first] = total;
+        total += (kv.second.size() + 63) & ~size_t(63);
+    }
+    for (int i = 0; i < rt->n_layers; ++i) {
+        if (rt->lq[i].x2_kind != 2) continue;
+        rt->lq[i].pos_off = total;
+        total += ((2 * pos[i].first.size()) + 63) & ~size_t(63);
+    }
+    std::vector<float> host(total ? total : 1, 0.0f);
+    for (const auto& kv : rt->w) std::memcpy(host.data() + rt->off[kv.first], kv.second.data(), kv.second.size() * 4);
+    for (int i = 0; i < rt->n_layers; ++i) {
+        if (rt->lq[i].x2_kind != 2) continue;
+        std::memcpy(host.data() + rt->lq[i].pos_off, pos[i].first.data(), pos[i].first.size() * 4);
+        std::memcpy(host.data() + rt->lq[i].pos_off + pos[i].first.size(), pos[i].second.data(),
+                    pos[i].second.size() * 4);
+    }
+    (void)hipGetDevice(&rt->device);
+    if (hipMalloc(&rt->dblock, host.size() * 4) != hipSuccess) {
+        rt->dblock = nullptr;
+        return set_error(NFLOW_INTERNAL, "runtime: device allocation of the weights failed");
+    }
+    if (hipMemcpy(rt->dblock, host.data(), host.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return set_error(NFLOW_INTERNAL, "runtime: weight upload failed");
+    return NFLOW_OK;
+}
+
+// Ensure `bytes` of workspace (not stream-ordered: waits for the device
+// before freeing a smaller one).
+int ensure_ws(nflow_runtime* rt, size_t bytes) {
+    if (bytes <= rt->ws_bytes) return NFLOW_OK;
+    if (rt->ws) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(rt->ws);
+        rt->ws = nullptr;
+        rt->ws_bytes = 0;
+    }
+    if (hipMalloc(&rt->ws, bytes) != hipSuccess) {
+        rt->ws = nullptr;
+        return set_error(NFLOW_INTERNAL, "runtime: workspace allocation failed");
+    }
+    rt->ws_bytes = bytes;
+    return NFLOW_OK;
+}
+
+const float* twiddle_table(nflow_runtime* rt, int n) {
+    auto it = rt->tw.find(n);
+    if (it != rt->tw.end()) return it->second;
+    std::vector<float> f, inv;
+    twiddles(n, false, f);
+    twiddles(n, true, inv);
+    float* d = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d), (f.size() + inv.size()) * 4) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, f.data(), f.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d + f.size(), inv.data(), inv.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    rt->tw[n] = d;
+    return d;
+}
+
+int check_shapes(const nflow_runtime* rt, const int64_t* xs, int xn, const int64_t* ys, int yn) {
+    // FNO1d::Forward's checks, in its order and with its messages (fno.cpp:409-425).
+    if (!xs || xn != 3) return set_error(NFLOW_SHAPE_MISMATCH, "expected 3D input (batch, n, in_ch)");
+    if (xs[2] != rt->in_ch) return set_error(NFLOW_SHAPE_MISMATCH, "input channels mismatch");
+    if (!ys || yn != 3 || ys[0] != xs[0] || ys[1] != xs[1] || ys[2] != rt->out_ch)
+        return set_error(NFLOW_SHAPE_MISMATCH, "output buffer shape mismatch");
+    if (!is_pow2(xs[1])) return set_error(NFLOW_INVALID_ARG, "Stage 1: input length n must be a power of two");
+    return NFLOW_OK;
+}
+
+int launch_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        return set_error(NFLOW_INTERNAL, std::string("runtime: ") + what + ": " + hipGetErrorString(e));
+    return NFLOW_OK;
+}
+
+// FNO1d::Forward on device buffers (fno.cpp:408-700).
+int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, hipStream_t st) {
+    const int64_t b = xs[0], n = xs[1];
+    const int w = rt->width;
+    int64_t n_pad = n;
+    if (rt->pad_factor > 1) {
+        const int64_t r = n % rt->pad_factor;
+        n_pad = n + (r == 0 ? 0 : rt->pad_factor - r);
+    }
+    if (!is_pow2(n_pad))
+        return set_error(NFLOW_INVALID_ARG, "runtime: the padded length is not a power of two (the FFT needs one)");
+    if (n_pad > kFftMaxPoints)
+        return set_error(NFLOW_UNSUPPORTED_OP, "runtime: grids longer than 8192 points are not supported");
+    if (rt->modes > n_pad / 2 + 1)
+        return set_error(NFLOW_INVALID_ARG, "runtime: modes exceed the n/2 + 1 bins of the grid");
+    if (b == 0) return NFLOW_OK;
+    const int64_t M = b * n_pad;
+    if (M > INT32_MAX) return set_error(NFLOW_INVALID_ARG, "runtime: batch * points exceeds the batched API's int");
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const LayerQuant& q = rt->lq[i];
+        if (q.x2_kind == 2 && (q.pos_width != w || q.pos_count < n_pad * w))
+            return set_error(NFLOW_SHAPE_MISMATCH, "runtime: per-token qparams of locs." + std::to_string(i) +
+                                                       ".output do not cover (points, width)");
+    }
+    const float* tw = twiddle_table(rt, static_cast<int>(n_pad));
+    if (!tw) return set_error(NFLOW_INTERNAL, "runtime: twiddle upload failed");
+    // Workspace: h, x1, x2 (M x w each) and the kept spectrum.
+    const size_t act_elems = static_cast<size_t>(M) * w;
+    const size_t spec_elems = static_cast<size_t>(b) * w * (rt->modes > 0 ? rt->modes : 1) * 2;
+    const size_t a64 = (act_elems + 63) & ~size_t(63);
+    if (int rc = ensure_ws(rt, (3 * a64 + spec_elems) * sizeof(float))) return rc;
+    float* H = static_cast<float*>(rt->ws);
+    float* X1 = H + a64;
+    float* X2 = X1 + a64;
+    float* SPEC = X2 + a64;
+
+    LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), H, b, static_cast<int>(n_pad), static_cast<int>(n),
+                 static_cast<int>(n), rt->in_ch, w, RT_ACT_NONE};
+    if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const LayerQuant& q = rt->lq[i];
+        const std::string si = std::to_string(i);
+        if (q.in_fq)
+            if (int rc = launch_check(launch_fake_quant(H, M * w, q.in_scale, q.in_zp, st), "input fake-quant"))
+                return rc;
+        int log2n = 0;
+        while ((int64_t(1) << log2n) < n_pad) ++log2n;
+        SpecArgs sp{H, SPEC, X1, rt->dw("specs." + si + ".weights_real"), rt->dw("specs." + si + ".weights_imag"),
+                    tw, tw + 2 * (n_pad > 1 ? n_pad - 1 : 1), b, static_cast<int>(n_pad), log2n, w, rt->modes,
+                    1.0f / static_cast<float>(n_pad)};
+        if (int rc = launch_check(launch_spectral(sp, st), "spectral convolution")) return rc;
+        if (q.int8 && rt->int8_enabled) {
+            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], M, H, X2, q.sa, q.zpa, st)) return rc;
+        } else {
+            LinArgs loc{H, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b,
+                        static_cast<int>(n_pad), static_cast<int>(n_pad), static_cast<int>(n_pad), w, w, RT_ACT_NONE};
+            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        }
+        PostArgs pa{};
+        pa.x2 = X2;
+        pa.x1 = X1;
+        pa.h = H;
+        pa.M = M;
+        pa.w = w;
+        pa.points = static_cast<int>(n_pad);
+        pa.kind = q.x2_kind;
+        pa.scale = q.x2_scale;
+        pa.zpf = static_cast<float>(q.x2_zp);
+        if (q.x2_kind == 2) {
+            pa.pos_scales = static_cast<const float*>(rt->dblock) + q.pos_off;
+            pa.pos_zps = reinterpret_cast<const int32_t*>(pa.pos_scales + q.pos_count);
+        }
+        std::memcpy(pa.thr, rt->thr, sizeof(pa.thr));
+        pa.act = rt->act;
+        if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
+    }
+    // Trim, proj_q + act, proj_out (fno.cpp:662-698).
+    LinArgs pq{H, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X1, b, static_cast<int>(n), static_cast<int>(n),
+               static_cast<int>(n_pad), w, w, rt->act};
+    if (int rc = launch_check(launch_linear_ref(pq, st), "proj_q")) return rc;
+    LinArgs po{X1, rt->dw("proj_out.weight"), rt->dw("proj_out.bias"), y, b, static_cast<int>(n), static_cast<int>(n),
+               static_cast<int>(n), w, rt->out_ch, RT_ACT_NONE};
+    return launch_check(launch_linear_ref(po, st), "proj_out");
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        int cur = 0;
+        if (hipGetDevice(&cur) == hipSuccess && cur != dev && hipSetDevice(dev) == hipSuccess) prev = cur;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+int create_from(nflow_ir* ir, nflow_runtime** out) {
+    nflow_runtime* rt = new (std::nothrow) nflow_runtime;
+    if (!rt) {
+        nflow_ir_close(ir);
+        return set_error(NFLOW_INTERNAL, "runtime: out of host memory");
+    }
+    rt->ir = ir;
+    if (int rc = init(rt)) {
+        const std::string msg = nflow_last_error();
+        free_runtime(rt);
+        return set_error(rc, msg);
+    }
+    *out = rt;
+    return NFLOW_OK;
+}
+
+}  // namespace
+}  // namespace nfq
+
+extern "C" {
+
+int nflow_runtime_create(const char* ir_path, nflow_runtime** out) {
+    clear_error();
+    if (!out) return set_error(NFLOW_INVALID_ARG, "runtime_create: null handle pointer");
+    *out = nullptr;
+    if (!ir_path) return set_error(NFLOW_INVALID_ARG, "runtime_create: null path");
+    nflow_ir* ir = nullptr;
+    if (int rc = nflow_ir_open(ir_path, &ir)) return rc;
+    return create_from(ir, out);
+}
+
+int nflow_runtime_create_memory(const void* data, size_t bytes, nflow_runtime** out) {
+    clear_error();
+    if (!out) return set_error(NFLOW_INVALID_ARG, "runtime_create_memory: null handle pointer");
+    *out = nullptr;
+    nflow_ir* ir = nullptr;
+    if (int rc = nflow_ir_open_memory(data, bytes, &ir)) return rc;
+    return create_from(ir, out);
+}
+
+int nflow_runtime_destroy(nflow_runtime* rt) {
+    clear_error();
+    free_runtime(rt);
+    return NFLOW_OK;
+}
+
+const char* nflow_runtime_op(const nflow_runtime* rt) { return rt ? rt->op.c_str() : ""; }
+
+int nflow_runtime_config(const nflow_runtime* rt, int32_t* config6, int* activation, int* quant_enabled) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_config: null runtime");
+    if (config6) {
+        const int32_t c[6] = {rt->in_ch, rt->out_ch, rt->width, rt->modes, rt->n_layers, rt->pad_factor};
+        std::memcpy(config6, c, sizeof(c));
+    }
+    if (activation) *activation = rt->act == RT_ACT_RELU ? NFLOW_ACT_RELU : NFLOW_ACT_GELU_TANH;
+    if (quant_enabled) *quant_enabled = rt->quant_enabled ? 1 : 0;
+    return NFLOW_OK;
+}
+
+int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm: null runtime");
+    DeviceGuard g(rt->device);
+    for (auto* l : rt->int8_layers) nflow_layer_destroy(l);
+    rt->int8_layers.assign(rt->n_layers, nullptr);
+    rt->int8_enabled = true;
+    // fno.cpp:360-406 caches lift / proj blobs too, but only locs.{i} is
+    // ever dispatched (fno.cpp:529-536); those are the ones built here.
+    for (int i = 0; i < rt->n_layers; ++i) {
+        LayerQuant& q = rt->lq[i];
+        q.int8 = false;
+        const std::string key = "locs." + std::to_string(i) + ".weight";
+        int found = 0, n_ch = 0, axis = 0;
+        const float* sc = nullptr;
+        const int32_t* zp = nullptr;
+        (void)nflow_ir_per_channel_qparam(rt->ir, key.c_str(), &found, &n_ch, &axis, &sc, &zp);
+        if (!found || axis != 0) continue;
+        const int w = rt->width;
+        if (n_ch < w) return set_error(NFLOW_SHAPE_MISMATCH, "runtime: fewer channel qparams than rows of " + key);
+        std::vector<int8_t> wq(static_cast<size_t>(w) * w);
+        std::vector<int32_t> sum(w);
+        if (int rc = nflow_host_quantise_weight_2d(rt->w[key].data(), w, w, sc, zp, wq.data(), sum.data())) return rc;
+        if (int rc = nflow_layer_create_int8(wq.data(), sc, zp, rt->w["locs." + std::to_string(i) + ".bias"].data(),
+                                             sum.data(), w, w, &rt->int8_layers[i]))
+            return rc;
+        // LinearDispatchTryInt8's conditions on the input key (fno.cpp:129-136).
+        int use = 0;
+        if (int rc = nflow_ir_fno_int8_dispatch(rt->ir, i, &use, &q.sa, &q.zpa)) return rc;
+        q.int8 = use != 0;
+    }
+    return NFLOW_OK;
+}
+
+int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled) {
+    clear_error();
+    if (!rt || !enabled) return set_error(NFLOW_INVALID_ARG, "runtime_is_int8_gemm_enabled: null argument");
+    *enabled = rt->int8_enabled ? 1 : 0;
+    return NFLOW_OK;
+}
+
+int nflow_runtime_layer_dispatch(const nflow_runtime* rt, int layer_index, int* uses_int8) {
+    clear_error();
+    if (!rt || !uses_int8) return set_error(NFLOW_INVALID_ARG, "runtime_layer_dispatch: null argument");
+    if (layer_index < 0 || layer_index >= rt->n_layers)
+        return set_error(NFLOW_INVALID_ARG, "runtime_layer_dispatch: layer index out of range");
+    *uses_int8 = (rt->int8_enabled && rt->lq[layer_index].int8) ? 1 : 0;
+    return NFLOW_OK;
+}
+
+int nflow_runtime_run_device(nflow_runtime* rt, const float* x, const int64_t* x_shape, int x_ndim, float* y,
+                             const int64_t* y_shape, int y_ndim, void* stream) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_run: null runtime");
+    if (int rc = check_shapes(rt, x_shape, x_ndim, y_shape, y_ndim)) return rc;
+    if (x_shape[0] > 0 && (!x || !y)) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
+    DeviceGuard g(rt->device);
+    return run_device(rt, x, x_shape, y, static_cast<hipStream_t>(stream));
+}
+
+int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape, int x_ndim, float* y,
+                      const int64_t* y_shape, int y_ndim) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_run: null runtime");
+    if (int rc = check_shapes(rt, x_shape, x_ndim, y_shape, y_ndim)) return rc;
+    const size_t nx = static_cast<size_t>(x_shape[0] * x_shape[1] * x_shape[2]);
+    const size_t ny = static_cast<size_t>(y_shape[0] * y_shape[1] * y_shape[2]);
+    if (nx == 0) return NFLOW_OK;
+    if (!x || !y) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
+    DeviceGuard g(rt->device);
+    float* dx = nullptr;
+    float* dy = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&dx), nx * 4) != hipSuccess) return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
+    if (hipMalloc(reinterpret_cast<void**>(&dy), ny * 4) != hipSuccess) {
+        (void)hipFree(dx);
+        return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
+    }
+    int rc = NFLOW_OK;
+    if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
+    if (!rc) rc = run_device(rt, dx, x_shape, dy, nullptr);
+    if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
+    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: device error");
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    return rc;
+}
+
+}  // extern "C"

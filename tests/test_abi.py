@@ -13,12 +13,17 @@ from neuroflow_amd import quant as Q
 from neuroflow_amd import workloads as WL
 from oracle import oracle as O
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "nflow_quant.h"
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+HEADER = INCLUDE / "nflow_quant.h"
 
 
 def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(nflow_\w+)\s*\(", text)))
+    names = set()
+    for h in sorted(INCLUDE.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = text.split("#ifdef __cplusplus\n}")[0]     # the C-ABI part (C++ wrappers follow it)
+        names |= set(re.findall(r"\b(nflow_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_the_expected_surface():
