@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch"])
+                    choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d"])
     ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", default=True)
@@ -173,6 +173,128 @@ def cpu_baseline(wl, layers, args):
     }
 
 
+def ref_runtime_baseline(model, threads_all):
+    """The reference runtime itself (InferenceRuntime over FNO1d with
+    EnableInt8Gemm, oracle/_ref/ref_fno_run built from its sources) on the
+    host cores over a bounded sample of the same batch."""
+    import subprocess
+    import tempfile
+
+    import numpy as np
+    from oracle import oracle as O
+
+    exe = ROOT / "oracle" / "_ref" / "ref_fno_run"
+    if not exe.exists():
+        raise FileNotFoundError(f"{exe} not built")
+    b_s = 16
+    x = np.ascontiguousarray(model.x[:b_s])
+    _, n, ci = x.shape
+    co = model.config[1]
+    with tempfile.TemporaryDirectory() as d:
+        ir, xf, yf = Path(d) / "m.nneuroir", Path(d) / "x.f32", Path(d) / "y.f32"
+        ir.write_bytes(model.ir)
+        x.tofile(xf)
+        rates = {}
+        for threads in (1, threads_all):
+            out = subprocess.run([str(exe), str(ir), str(xf), str(b_s), str(n), str(ci), str(co), str(yf), "int8",
+                                  "3", str(threads)], capture_output=True, text=True, check=True).stdout
+            us = float(out.split("us_per_run")[1].split()[0])
+            rates[threads] = b_s / (us * 1e-6)
+    return {"value": rates[threads_all], "unit": "samples/s", "cores": threads_all, "kind": "reference",
+            "sample": (f"InferenceRuntime::Run with EnableInt8Gemm (the reference runtime built from its "
+                       f"sources: runtime.cpp, fno.cpp, fft.cpp, int8_gemm.cpp VNNI) on {b_s} of the "
+                       f"batch's samples, median of 3 runs, samples split over {threads_all} threads with "
+                       f"one runtime each, and on 1 thread; host {O.host_cpu_model()}"),
+            "value_1core": rates[1]}
+
+
+def bench_fno1d_model(args):
+    """The whole FNO1d model through the device runtime: one step = one
+    InferenceRuntime run (lift, 4 x [input fake-quant, spectral convolution,
+    INT8 local-linear layer, act(x1 + x2)], proj_q, proj_out) over the batch,
+    with its input already in HBM."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+    from neuroflow_amd import _lib
+    from neuroflow_amd import workloads as WL
+
+    L = _lib.lib()
+    dev = torch.device("cuda:0")
+    model = WL.fno1d_model()
+    h = C.c_void_p()
+    buf = C.create_string_buffer(model.ir, len(model.ir))
+    _lib.check(L.nflow_runtime_create_memory(buf, len(model.ir), C.byref(h)), "runtime_create")
+    _lib.check(L.nflow_runtime_enable_int8_gemm(h), "runtime_enable_int8_gemm")
+    b, n, ci = model.x.shape
+    co = model.config[1]
+    xsh = (C.c_int64 * 3)(b, n, ci)
+    ysh = (C.c_int64 * 3)(b, n, co)
+    n_sets = 4
+    xs = [torch.from_numpy(model.x).to(dev) for _ in range(n_sets)]
+    ys = [torch.empty(b, n, co, dtype=torch.float32, device=dev) for _ in range(n_sets)]
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+    fn = L.nflow_runtime_run_device
+
+    def step(i):
+        _lib.check(fn(h, xs[i % n_sets].data_ptr(), xsh, 3, ys[i % n_sets].data_ptr(), ysh, 3, sptr),
+                   "runtime_run_device")
+
+    for i in range(max(1, args.warmup)):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    parity = None
+    if args.check:
+        from oracle import fno1d as OF
+        m = OF.from_records(model.config, False, model.weights, model.qparams)
+        OF.enable_int8_gemm(m)
+        want = OF.forward(m, model.x[:2])
+        y2 = torch.empty(2, n, co, dtype=torch.float32, device=dev)
+        _lib.check(fn(h, xs[0].data_ptr(), (C.c_int64 * 3)(2, n, ci), 3, y2.data_ptr(),
+                      (C.c_int64 * 3)(2, n, co), 3, sptr), "runtime_run_device")
+        torch.cuda.synchronize()
+        parity = bool(np.array_equal(y2.cpu().numpy().view(np.uint32), want.view(np.uint32)))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            from oracle import oracle as O
+            cpu = ref_runtime_baseline(model, O.usable_cores())
+        except Exception as e:  # reported, not fatal
+            cpu = {"error": f"{type(e).__name__}: {e}"}
+    L.nflow_runtime_destroy(h)
+    out = {
+        "metric": METRIC,
+        "value": round(b / (ms_per_step * 1e-3), 2),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded SplitMix64 input fields, seeded PyTorch-style initial weights)",
+        "config": {"workload": model.name, "batch": b, "points": n, "config": model.config,
+                   "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
+    }
+    print(json.dumps(out))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -180,6 +302,9 @@ def main():
               "(the path shards along rows with no collective; see the design notes)",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "fno1d":
+        bench_fno1d_model(args)
+        return
 
     import numpy as np
     import torch

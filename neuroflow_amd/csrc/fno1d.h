@@ -2,11 +2,13 @@
 // called by the host runtime (runtime.cpp).  Every launcher is stream-ordered
 // and returns hipError_t of the launch.
 //
-// Layout: activations are token-major, (samples, points, width) with width
-// contiguous -- the layout the local-linear kernels read -- where the
-// reference keeps (samples, width, points) and permutes around its Linear
-// (fno.cpp:437-445, 523-556).  Only the layout differs: every element is
-// computed by the same float operations as the reference build.
+// Layouts: the local-linear layers read and write token-major activations,
+// (samples, points, width) with width contiguous; the spectral convolution
+// reads and writes channel-major ones, (samples, width, points) with points
+// contiguous -- the reference's layout (fno.cpp:437-445, 523-556).  The layer
+// tail writes the new activation in both.  Only the layout differs from the
+// reference: every element is computed by the same float operations as its
+// x86 build.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -22,10 +24,11 @@ enum RtAct { RT_ACT_NONE = 0, RT_ACT_RELU = 1, RT_ACT_GELU = 2 };
 constexpr int kFftMaxPoints = 8192;
 
 // y (samples, rows_out, n) = act(b + x W^T) in the reference Linear's
-// summation order (fno.cpp:69-79 as compiled: blocks of 16 / 8 rounded
-// products, the last k % 8 terms fused).  Row t of sample s reads input row
-// s * rows_in + t; rows t >= rows_valid are written as 0 (the zero padding
-// of fno.cpp:449-466).  W is (n, k) row-major, b may be null.
+// summation order (fno.cpp:69-79 as its build computes it: the first
+// k - k % 8 products rounded and added in order, the last k % 8 fused).
+// Row t of sample s reads input row s * rows_in + t; rows t >= rows_valid
+// are written as 0 (the zero padding of fno.cpp:449-466).  W is (n, k)
+// row-major, b may be null.
 struct LinArgs {
     const float* x;
     const float* W;
@@ -41,22 +44,31 @@ struct LinArgs {
 };
 hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st);
 
-// In-place INT8 fake-quant round trip of n elements (fno.cpp:488-501).
-hipError_t launch_fake_quant(float* h, int64_t n, float scale, int32_t zp, hipStream_t st);
+// The INT8 fake-quant of an activation (fno.cpp:488-501), optional.
+struct FakeQuant {
+    int on;
+    float scale;
+    float zpf;
+};
 
-// Spectral convolution of fno.cpp:164-207 on token-major h (samples, n, w):
-// forward FFT of every channel (radix-2, fft.cpp:48-84) keeping bins
-// 0 .. modes-1 in spec (samples, w, modes) complex, then per output channel
-// the channel mix (in, out, modes weights) and the inverse FFT
-// (fft.cpp:86-100), written token-major to x1.  tw_fwd / tw_inv hold the
-// stage twiddles: stage of length len at entries len/2 - 1 .. len - 2
-// (n - 1 complex values per table).
+// Token-major h (samples, n, w) to channel-major hc (samples, w, n), with the
+// input fake-quant fq applied to both when on.
+hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,
+                                   hipStream_t st);
+
+// Spectral convolution of fno.cpp:164-207 on channel-major hc: forward FFT
+// of every channel (radix-2, fft.cpp:48-84) keeping bins 0 .. modes-1 in
+// spec (samples, w, modes) complex, the channel mix into spec_mixed, and per
+// output channel the inverse FFT (fft.cpp:86-100) into channel-major x1c.
+// tw_fwd / tw_inv: the stage twiddles, stage of length len at entries
+// len/2 - 1 .. len - 2 (n - 1 complex values per table).
 struct SpecArgs {
-    const float* h;
-    float* spec;
-    float* x1;
-    const float* w_real;
-    const float* w_imag;
+    const float* hc;
+    float* spec;          // forward bins (samples, w, modes) complex
+    float* spec_mixed;    // mixed bins (samples, w, modes) complex
+    float* x1c;
+    const float* mix_real;  // the spectral weights held (modes, in, out)
+    const float* mix_imag;
     const float* tw_fwd;
     const float* tw_inv;
     int64_t samples;
@@ -68,17 +80,20 @@ struct SpecArgs {
 };
 hipError_t launch_spectral(const SpecArgs& a, hipStream_t st);
 
-// The layer tail h = act(x1 + fq(x2)) (fno.cpp:558-660) on token-major
-// (M, w) buffers.  kind 0 none, 1 per-tensor INT8, 2 per-position INT8
-// (index column * points + row % points, the reference's indexing),
-// 3 the log2 snap of fno.cpp:579-606 with its exponent step points in thr.
+// The layer tail h = act(x1 + fq(x2)) (fno.cpp:558-660) from token-major x2
+// and channel-major x1c, written to token-major h and channel-major hc, with
+// the next layer's input fake-quant (fq_next) applied.  kind 0 none,
+// 1 per-tensor INT8, 2 per-position INT8 (index column * points + position,
+// the reference's indexing), 3 the log2 snap of fno.cpp:579-606 with its
+// exponent step points in thr.
 struct PostArgs {
     const float* x2;
-    const float* x1;
+    const float* x1c;
     float* h;
-    int64_t M;
+    float* hc;
+    int64_t samples;
+    int n;
     int w;
-    int points;
     int kind;
     float scale;
     float zpf;
@@ -86,6 +101,7 @@ struct PostArgs {
     const int32_t* pos_zps;
     float thr[15];
     int act;
+    FakeQuant fq_next;
 };
 hipError_t launch_post(const PostArgs& a, hipStream_t st);
 

@@ -44,50 +44,194 @@ __device__ __forceinline__ int64_t xcd_block(int64_t nlogical) {
 }
 
 // ---------------------------------------------------------------------------
-// fp32 Linear (fno.cpp:69-79) in the reference build's summation order.
+// fp32 Linear (fno.cpp:69-79) in the reference build's summation order: the
+// first k - k % 8 products rounded and added one by one, the rest fused.
 // ---------------------------------------------------------------------------
-template <bool LDSW>
-__global__ __launch_bounds__(256) void k_linear_ref(LinArgs a) {
-    extern __shared__ float wt[];  // W transposed: wt[p * n + j] = W[j][p]
-    const int k = a.k, n = a.n;
-    if constexpr (LDSW) {
-        for (int i = threadIdx.x; i < k * n; i += blockDim.x) wt[(i % k) * n + i / k] = a.W[i];
-        __syncthreads();
+__device__ __forceinline__ float lin_step(float acc, float x, float w, bool plain) {
+    return plain ? acc + x * w : __builtin_fmaf(x, w, acc);
+}
+
+// k == 64, n >= 16: one wave per 4 output rows; lane j holds column j of W
+// in registers (chunks of 64 columns), the rows' inputs go through LDS and
+// are read back as broadcasts.
+__global__ __launch_bounds__(256) void k_linear_rows64(LinArgs a) {
+    __shared__ v4f xs[4][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int n = a.n;
+    const int64_t rows = a.samples * a.rows_out;
+    const int64_t quads = (rows + 3) / 4;
+    const int64_t wave0 = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    const float* xsf = reinterpret_cast<const float*>(xs[wid]);
+    for (int cc = 0; cc < n; cc += 64) {
+        const int j = cc + lane;
+        const bool jv = j < n;
+        float wr[64];
+        const float* wj = a.W + static_cast<int64_t>(jv ? j : 0) * 64;
+#pragma unroll
+        for (int p = 0; p < 64; p += 4) {
+            const v4f q = *reinterpret_cast<const v4f*>(wj + p);
+            wr[p] = q[0];
+            wr[p + 1] = q[1];
+            wr[p + 2] = q[2];
+            wr[p + 3] = q[3];
+        }
+        const float bj = (jv && a.b) ? a.b[j] : 0.0f;
+        for (int64_t qd = wave0; qd < quads; qd += nwaves) {
+            // Lane l loads 4 inputs of row 4 qd + l / 16.
+            {
+                const int64_t r = qd * 4 + (lane >> 4);
+                v4f v = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (r < rows) {
+                    const int64_t s = r / a.rows_out;
+                    const int t = static_cast<int>(r % a.rows_out);
+                    if (t < a.rows_valid)
+                        v = *reinterpret_cast<const v4f*>(a.x + (s * a.rows_in + t) * 64 + 4 * (lane & 15));
+                }
+                xs[wid][lane] = v;
+            }
+            wave_sync();
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t r = qd * 4 + rr;
+                if (r >= rows) break;
+                const int t = static_cast<int>(r % a.rows_out);
+                float out = 0.0f;
+                if (t < a.rows_valid) {
+                    float acc = bj;
+#pragma unroll
+                    for (int p = 0; p < 64; ++p) acc = acc + xsf[rr * 64 + p] * wr[p];
+                    out = rt_activate(acc, a.act);
+                }
+                if (jv) a.y[r * n + j] = out;
+            }
+            wave_sync();
+        }
     }
+}
+
+// n <= 16: one thread per output row, all n columns in registers, W from LDS.
+template <int NMAX>
+__global__ __launch_bounds__(256) void k_linear_narrow(LinArgs a) {
+    extern __shared__ float ws[];   // W (n, k) row-major
+    const int k = a.k, n = a.n, kplain = k - k % 8;
+    for (int i = threadIdx.x; i < n * k; i += blockDim.x) ws[i] = a.W[i];
+    __syncthreads();
+    const bool vec4 = (k % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0);
+    const int64_t rows = a.samples * a.rows_out;
+    for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < rows;
+         r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const uint32_t ro = static_cast<uint32_t>(a.rows_out);
+        const int64_t s = rows < (int64_t(1) << 32) ? static_cast<uint32_t>(r) / ro : r / a.rows_out;
+        const int t = static_cast<int>(r - s * a.rows_out);
+        float acc[NMAX];
+#pragma unroll
+        for (int j = 0; j < NMAX; ++j) acc[j] = (j < n && a.b) ? a.b[j] : 0.0f;
+        if (t < a.rows_valid) {
+            const float* xr = a.x + (s * a.rows_in + t) * static_cast<int64_t>(k);
+            int p = 0;
+            if (vec4) {
+                for (; p + 4 <= k; p += 4) {
+                    const v4f xv = *reinterpret_cast<const v4f*>(xr + p);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int j = 0; j < NMAX; ++j)
+                            if (j < n) acc[j] = lin_step(acc[j], xv[q], ws[j * k + p + q], p + q < kplain);
+                }
+            }
+            for (; p < k; ++p) {
+                const float xv = xr[p];
+                const bool plain = p < kplain;
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j)
+                    if (j < n) acc[j] = lin_step(acc[j], xv, ws[j * k + p], plain);
+            }
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j)
+                if (j < n) a.y[r * n + j] = rt_activate(acc[j], a.act);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j)
+                if (j < n) a.y[r * n + j] = 0.0f;
+        }
+    }
+}
+
+// Any shape: one thread per output.
+__global__ __launch_bounds__(256) void k_linear_flat(LinArgs a) {
+    const int k = a.k, n = a.n, kplain = k - k % 8;
     const int64_t total = a.samples * a.rows_out * static_cast<int64_t>(n);
+    const bool narrow_idx = total < (int64_t(1) << 32);
     for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
          idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int j = static_cast<int>(idx % n);
-        const int64_t r = idx / n;
-        const int64_t s = r / a.rows_out;
-        const int t = static_cast<int>(r % a.rows_out);
+        int64_t r, s;
+        if (narrow_idx) {
+            const uint32_t r32 = static_cast<uint32_t>(idx) / static_cast<uint32_t>(n);
+            r = r32;
+            s = r32 / static_cast<uint32_t>(a.rows_out);
+        } else {
+            r = idx / n;
+            s = r / a.rows_out;
+        }
+        const int j = static_cast<int>(idx - r * n);
+        const int t = static_cast<int>(r - s * a.rows_out);
         float out = 0.0f;
         if (t < a.rows_valid) {
             const float* xr = a.x + (s * a.rows_in + t) * static_cast<int64_t>(k);
             const float* wr = a.W + static_cast<int64_t>(j) * k;
-            auto wv = [&](int p) { return LDSW ? wt[p * n + j] : wr[p]; };
             float acc = a.b ? a.b[j] : 0.0f;
-            int p = 0;
-            for (; p + 16 <= k; p += 16)
-#pragma unroll
-                for (int q = 0; q < 16; ++q) acc = acc + xr[p + q] * wv(p + q);
-            if (k - p >= 8) {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) acc = acc + xr[p + q] * wv(p + q);
-                p += 8;
-            }
-            for (; p < k; ++p) acc = __builtin_fmaf(xr[p], wv(p), acc);
+            for (int p = 0; p < k; ++p) acc = lin_step(acc, xr[p], wr[p], p < kplain);
             out = rt_activate(acc, a.act);
         }
         a.y[r * n + j] = out;
     }
 }
 
-// fno.cpp:488-501: q = std::round(v / s) + zp, clamped, then (q - zp) * s.
-__global__ __launch_bounds__(256) void k_fake_quant(float* h, int64_t n, float s, float zpf) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-        h[i] = x2_fake_quant(h[i], s, zpf);
+// ---------------------------------------------------------------------------
+// Layout change and the layer tail, on 64-point x 64-channel tiles.
+// ---------------------------------------------------------------------------
+struct Tile {
+    int64_t s;
+    int t0, c0;
+};
+
+__device__ __forceinline__ bool tile_of(int64_t id, int64_t samples, int n, int w, Tile& tl) {
+    const int tt = (n + 63) / 64, tc = (w + 63) / 64;
+    const int64_t per_sample = static_cast<int64_t>(tt) * tc;
+    if (id >= samples * per_sample) return false;
+    tl.s = id / per_sample;
+    const int rem = static_cast<int>(id % per_sample);
+    tl.t0 = (rem / tc) * 64;
+    tl.c0 = (rem % tc) * 64;
+    return true;
+}
+
+__device__ __forceinline__ float apply_fq(float v, FakeQuant q) {
+    return q.on ? x2_fake_quant(v, q.scale, q.zpf) : v;
+}
+
+__global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, int64_t samples, int n, int w,
+                                                          FakeQuant fq) {
+    __shared__ float tile[64][65];
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of(id, samples, n, w, tl); id += gridDim.x) {
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            if (t < n && c < w) {
+                const int64_t o = (tl.s * n + t) * w + c;
+                const float v = apply_fq(h[o], fq);
+                if (fq.on) h[o] = v;
+                tile[cr][tr] = v;
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            if (t < n && c < w) hc[(tl.s * w + c) * n + t] = tile[cr][tr];
+        }
+        __syncthreads();
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -102,79 +246,213 @@ __device__ __forceinline__ float2 cmul_ref(float2 x, float2 w) {
     return make_float2(__builtin_fmaf(x.x, w.x, -(x.y * w.y)), __builtin_fmaf(x.x, w.y, x.y * w.x));
 }
 
-// The stages of fft.cpp:50-64 on a (already in bit-reversed order); the
-// butterflies of a stage are independent, spread over the wave's lanes.
-__device__ __forceinline__ void fft_stages(float2* a, int n, int log2n, const float2* tw, int lane) {
-    for (int lh = 0; lh < log2n; ++lh) {
-        const int half = 1 << lh;
-        const float2* twl = tw + (half - 1);
-        for (int q = lane; q < (n >> 1); q += 64) {
-            const int kk = q & (half - 1);
-            const int i = ((q >> lh) << (lh + 1)) + kk;
-            const float2 u = a[i];
-            const float2 v = cmul_ref(a[i + half], twl[kk]);
-            a[i] = make_float2(u.x + v.x, u.y + v.y);
-            a[i + half] = make_float2(u.x - v.x, u.y - v.y);
+// The stages of fft.cpp:50-64, P at a time: a pass takes the G = 2^P
+// elements of a group (spaced h0 apart in the bit-reversed array) into
+// registers and runs the butterflies of the stages with halves h0 .. 2^(P-1)
+// h0 on them -- the same butterflies, in the same order per element, as
+// the radix-2 loop.  Element e of the group at position base + e h0 sits at
+// local index kk + (e mod 2^(st+1)) h0 of its stage-st block, so its twiddle
+// is tw[h - 1 + kk + (e mod 2^st) h0].
+//   SRC 0: LDS buf; 1: the channel's real input, bit-reversed on load;
+//          2: the mixed spectrum, bins above n/2 the conjugates of those
+//             below (fft.cpp:86-96), bins >= modes zero ((0, 0) below n/2,
+//             their mirrors (0, -0));
+//   DST 0: LDS buf; 1: bins < modes to the kept spectrum; 2: real parts
+//          times 1/n to the channel's output.
+struct FftIo {
+    float2* buf;
+    const float2* tw;
+    const float* src_real;
+    const float2* src_spec;
+    float2* dst_spec;
+    float* dst_real;
+    int n;
+    int log2n;
+    int modes;
+    float inv_n;
+};
+
+template <int SRC>
+__device__ __forceinline__ float2 fft_load(const FftIo& io, int e) {
+    if constexpr (SRC == 0) {
+        return io.buf[e];
+    } else {
+        const int k = bit_rev(e, io.log2n);
+        if constexpr (SRC == 1) {
+            return make_float2(io.src_real[k], 0.0f);
+        } else {
+            const int nh = io.n >> 1;
+            if (k <= nh) return k < io.modes ? io.src_spec[k] : make_float2(0.0f, 0.0f);
+            const int kk = io.n - k;
+            if (kk < io.modes) {
+                const float2 v = io.src_spec[kk];
+                return make_float2(v.x, -v.y);
+            }
+            return make_float2(0.0f, -0.0f);
+        }
+    }
+}
+
+template <int DST>
+__device__ __forceinline__ void fft_store(const FftIo& io, int e, float2 v) {
+    if constexpr (DST == 0) {
+        io.buf[e] = v;
+    } else if constexpr (DST == 1) {
+        if (e < io.modes) io.dst_spec[e] = v;
+    } else {
+        io.dst_real[e] = v.x * io.inv_n;
+    }
+}
+
+template <int P, int SRC, int DST>
+__device__ __forceinline__ void fft_pass(const FftIo& io, int h0, int lane) {
+    constexpr int G = 1 << P;
+    const int ngroups = io.n >> P;
+    const int lh0 = __builtin_ctz(static_cast<unsigned>(h0));
+    for (int gq = lane; gq < ngroups; gq += 64) {
+        const int kk = gq & (h0 - 1);
+        const int base = ((gq >> lh0) << (lh0 + P)) + kk;
+        float2 v[G];
+#pragma unroll
+        for (int e = 0; e < G; ++e) v[e] = fft_load<SRC>(io, base + e * h0);
+#pragma unroll
+        for (int st = 0; st < P; ++st) {
+            const int span = 1 << st;
+            const int h = h0 << st;
+#pragma unroll
+            for (int e = 0; e < G; ++e) {
+                if (e & span) continue;
+                const float2 w = io.tw[h - 1 + kk + (e & (span - 1)) * h0];
+                const float2 t = cmul_ref(v[e + span], w);
+                const float2 u = v[e];
+                v[e] = make_float2(u.x + t.x, u.y + t.y);
+                v[e + span] = make_float2(u.x - t.x, u.y - t.y);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < G; ++e) fft_store<DST>(io, base + e * h0, v[e]);
+    }
+}
+
+template <int P, int SRC>
+__device__ __forceinline__ void fft_pass_to(const FftIo& io, int h0, int lane, bool last, int dst_last) {
+    if (!last) fft_pass<P, SRC, 0>(io, h0, lane);
+    else if (dst_last == 1) fft_pass<P, SRC, 1>(io, h0, lane);
+    else fft_pass<P, SRC, 2>(io, h0, lane);
+}
+
+// The whole transform of one channel by one wave: the first pass reads the
+// source (SRC), the last writes the destination (dst_last), the others go
+// through the wave's LDS buffer.
+template <int SRC>
+__device__ void fft_run(const FftIo& io, int lane, int dst_last) {
+    const int L = io.log2n;
+    if (L == 0) {
+        const float2 v = fft_load<SRC>(io, 0);
+        if (dst_last == 1) fft_store<1>(io, 0, v);
+        else fft_store<2>(io, 0, v);
+        return;
+    }
+    int done = 0, h0 = 1;
+    while (done < L) {
+        const int P = (L - done) >= 3 ? 3 : (L - done);
+        const bool last = done + P == L;
+        if (done == 0) {
+            if (P == 3) fft_pass_to<3, SRC>(io, h0, lane, last, dst_last);
+            else if (P == 2) fft_pass_to<2, SRC>(io, h0, lane, last, dst_last);
+            else fft_pass_to<1, SRC>(io, h0, lane, last, dst_last);
+        } else {
+            if (P == 3) fft_pass_to<3, 0>(io, h0, lane, last, dst_last);
+            else if (P == 2) fft_pass_to<2, 0>(io, h0, lane, last, dst_last);
+            else fft_pass_to<1, 0>(io, h0, lane, last, dst_last);
         }
         wave_sync();
+        done += P;
+        h0 <<= P;
     }
 }
 
-// Forward FFT of channel c of sample s (token-major h), bins 0 .. modes-1 to spec.
-template <int WPB>
+// Stage the block's twiddle table in LDS (TWL) before any wave leaves.
+template <bool TWL>
+__device__ __forceinline__ const float2* block_twiddles(float2* smem, const float* tw, int n) {
+    if constexpr (TWL) {
+        const float2* src = reinterpret_cast<const float2*>(tw);
+        for (int i = threadIdx.x; i < n - 1; i += blockDim.x) smem[i] = src[i];
+        __syncthreads();
+        return smem;
+    } else {
+        return reinterpret_cast<const float2*>(tw);
+    }
+}
+
+// Forward FFT of channel c of sample s (channel-major hc), bins 0 .. modes-1 to spec.
+template <int WPB, bool TWL>
 __global__ __launch_bounds__(64 * WPB) void k_rfft_modes(SpecArgs a, int64_t nlogical) {
-    extern __shared__ float2 fbuf[];
+    extern __shared__ float2 fsm[];
+    const int n = a.n;
+    const float2* tw = block_twiddles<TWL>(fsm, a.tw_fwd, n);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int64_t lb = xcd_block(nlogical);
     if (lb < 0) return;
     const int64_t item = lb * WPB + wid;
     if (item >= a.samples * a.w) return;
-    const int64_t s = item / a.w;
-    const int c = static_cast<int>(item % a.w);
-    const int n = a.n;
-    float2* buf = fbuf + static_cast<int64_t>(wid) * n;
-    for (int t = lane; t < n; t += 64)
-        buf[bit_rev(t, a.log2n)] = make_float2(a.h[(s * n + t) * a.w + c], 0.0f);
-    wave_sync();
-    fft_stages(buf, n, a.log2n, reinterpret_cast<const float2*>(a.tw_fwd), lane);
-    float2* spec = reinterpret_cast<float2*>(a.spec) + (s * a.w + c) * a.modes;
-    for (int m = lane; m < a.modes; m += 64) spec[m] = buf[m];
+    FftIo io{};
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.tw = tw;
+    io.src_real = a.hc + item * n;
+    io.dst_spec = reinterpret_cast<float2*>(a.spec) + item * a.modes;
+    io.n = n;
+    io.log2n = a.log2n;
+    io.modes = a.modes;
+    fft_run<1>(io, lane, 1);
 }
 
-// Channel mix (fno.cpp:176-198) and inverse FFT (fft.cpp:86-100) for output
-// channel wo of sample s, written token-major to x1.
-template <int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_mix_irfft(SpecArgs a, int64_t nlogical) {
-    extern __shared__ float2 fbuf[];
+// Channel mix (fno.cpp:176-198): out[s][wo][m] = sum over wi, in order, of
+// H[s][wi][m] * W[wi][wo][m] with the reference build's fused terms; the
+// weights are held (m, wi, wo) so a wave's 64 output channels read 256
+// contiguous bytes per wi.
+__global__ __launch_bounds__(256) void k_spec_mix(SpecArgs a, const float* mix_r, const float* mix_i,
+                                                  float* spec_out) {
+    const int m = blockIdx.z;
+    const int w = a.w, modes = a.modes;
+    const int wo = blockIdx.y * 64 + (threadIdx.x & 63);
+    const int64_t s = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wo >= w || s >= a.samples) return;
+    const float2* H = reinterpret_cast<const float2*>(a.spec) + s * w * modes + m;
+    const float* Wr = mix_r + static_cast<int64_t>(m) * w * w + wo;
+    const float* Wi = mix_i + static_cast<int64_t>(m) * w * w + wo;
+    float sr = 0.0f, si = 0.0f;
+    for (int k = 0; k < w; ++k) {
+        const float2 hv = H[static_cast<int64_t>(k) * modes];
+        const float wr = Wr[static_cast<int64_t>(k) * w], wim = Wi[static_cast<int64_t>(k) * w];
+        sr = sr + __builtin_fmaf(-wim, hv.y, hv.x * wr);
+        si = si + __builtin_fmaf(wr, hv.y, hv.x * wim);
+    }
+    reinterpret_cast<float2*>(spec_out)[(s * w + wo) * modes + m] = make_float2(sr, si);
+}
+
+// Inverse FFT (fft.cpp:86-100) of output channel wo of sample s from the
+// mixed spectrum, written channel-major to x1c.
+template <int WPB, bool TWL>
+__global__ __launch_bounds__(64 * WPB) void k_irfft(SpecArgs a, const float* spec_mixed, int64_t nlogical) {
+    extern __shared__ float2 fsm[];
+    const int n = a.n;
+    const float2* tw = block_twiddles<TWL>(fsm, a.tw_inv, n);
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int64_t lb = xcd_block(nlogical);
     if (lb < 0) return;
     const int64_t item = lb * WPB + wid;
     if (item >= a.samples * a.w) return;
-    const int64_t s = item / a.w;
-    const int wo = static_cast<int>(item % a.w);
-    const int n = a.n, w = a.w, modes = a.modes, nh = n >> 1;
-    float2* buf = fbuf + static_cast<int64_t>(wid) * n;
-    // Bins the mix leaves at zero: (0, 0) up to n/2, their conjugate
-    // mirrors (0, -0) above it.
-    for (int i = lane; i < n; i += 64) buf[bit_rev(i, a.log2n)] = make_float2(0.0f, i > nh ? -0.0f : 0.0f);
-    wave_sync();
-    const float2* spec = reinterpret_cast<const float2*>(a.spec) + s * w * modes;
-    for (int m = lane; m < modes; m += 64) {
-        float sr = 0.0f, si = 0.0f;
-        for (int k = 0; k < w; ++k) {
-            const float2 hv = spec[static_cast<int64_t>(k) * modes + m];
-            const int64_t wi = (static_cast<int64_t>(k) * w + wo) * modes + m;
-            const float wr = a.w_real[wi], wim = a.w_imag[wi];
-            sr = sr + __builtin_fmaf(-wim, hv.y, hv.x * wr);
-            si = si + __builtin_fmaf(wr, hv.y, hv.x * wim);
-        }
-        buf[bit_rev(m, a.log2n)] = make_float2(sr, si);
-        if (m >= 1 && m <= nh - 1) buf[bit_rev(n - m, a.log2n)] = make_float2(sr, -si);
-    }
-    wave_sync();
-    fft_stages(buf, n, a.log2n, reinterpret_cast<const float2*>(a.tw_inv), lane);
-    for (int t = lane; t < n; t += 64) a.x1[(s * n + t) * w + wo] = buf[t].x * a.inv_n;
+    FftIo io{};
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.tw = tw;
+    io.src_spec = reinterpret_cast<const float2*>(spec_mixed) + item * a.modes;
+    io.dst_real = a.x1c + item * n;
+    io.n = n;
+    io.log2n = a.log2n;
+    io.modes = a.modes;
+    io.inv_n = a.inv_n;
+    fft_run<2>(io, lane, 2);
 }
 
 // ---------------------------------------------------------------------------
@@ -206,21 +484,39 @@ __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
 }
 
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
-    const int64_t total = a.M * a.w;
-    for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
-         idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        float x2 = a.x2[idx];
-        if (a.kind == 1) {
-            x2 = x2_fake_quant(x2, a.scale, a.zpf);
-        } else if (a.kind == 2) {
-            const int64_t m = idx / a.w;
-            const int j = static_cast<int>(idx % a.w);
-            const int64_t p = static_cast<int64_t>(j) * a.points + m % a.points;
-            x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
-        } else if (a.kind == 3) {
-            x2 = log2_snap(x2, a.scale, a.thr);
+    __shared__ float tx1[64][65];  // x1, then (in place, same thread) the new h
+    const int n = a.n, w = a.w;
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of(id, a.samples, n, w, tl); id += gridDim.x) {
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            if (t < n && c < w) tx1[cr][tr] = a.x1c[(tl.s * w + c) * n + t];
         }
-        a.h[idx] = rt_activate(a.x1[idx] + x2, a.act);
+        __syncthreads();
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            if (t < n && c < w) {
+                const int64_t o = (tl.s * n + t) * w + c;
+                float x2 = a.x2[o];
+                if (a.kind == 1) {
+                    x2 = x2_fake_quant(x2, a.scale, a.zpf);
+                } else if (a.kind == 2) {
+                    const int64_t p = static_cast<int64_t>(c) * n + t;
+                    x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
+                } else if (a.kind == 3) {
+                    x2 = log2_snap(x2, a.scale, a.thr);
+                }
+                const float hv = apply_fq(rt_activate(tx1[cr][tr] + x2, a.act), a.fq_next);
+                a.h[o] = hv;
+                tx1[cr][tr] = hv;
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            if (t < n && c < w) a.hc[(tl.s * w + c) * n + t] = tx1[cr][tr];
+        }
+        __syncthreads();
     }
 }
 
@@ -229,45 +525,60 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
 // ---------------------------------------------------------------------------
 
 hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st) {
-    const int64_t total = a.samples * a.rows_out * static_cast<int64_t>(a.n);
-    if (total <= 0) return hipSuccess;
-    const unsigned grid = grid_for(total, 256, 8);
-    const size_t wbytes = static_cast<size_t>(a.k) * a.n * sizeof(float);
-    if (wbytes <= 48 * 1024)
-        hipLaunchKernelGGL(k_linear_ref<true>, dim3(grid), dim3(256), wbytes, st, a);
-    else
-        hipLaunchKernelGGL(k_linear_ref<false>, dim3(grid), dim3(256), 0, st, a);
+    const int64_t rows = a.samples * a.rows_out;
+    if (rows <= 0 || a.n <= 0) return hipSuccess;
+    if (a.k == 64 && a.n >= 16 && aligned(a.x, 16) && aligned(a.W, 16)) {
+        hipLaunchKernelGGL(k_linear_rows64, dim3(grid_for((rows + 3) / 4, 4, 8)), dim3(256), 0, st, a);
+    } else if (a.n <= 16 && static_cast<size_t>(a.n) * a.k * sizeof(float) <= 48 * 1024) {
+        hipLaunchKernelGGL(k_linear_narrow<16>, dim3(grid_for(rows, 256, 8)), dim3(256),
+                           static_cast<size_t>(a.n) * a.k * sizeof(float), st, a);
+    } else {
+        hipLaunchKernelGGL(k_linear_flat, dim3(grid_for(rows * a.n, 256, 8)), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_fake_quant(float* h, int64_t n, float scale, int32_t zp, hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_fake_quant, dim3(grid_for(n, 256, 8)), dim3(256), 0, st, h, n, scale,
-                       static_cast<float>(zp));
+static unsigned tile_grid(int64_t samples, int n, int w) {
+    const int64_t tiles = samples * ((n + 63) / 64) * static_cast<int64_t>((w + 63) / 64);
+    return grid_for(tiles, 1, 8);
+}
+
+hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,
+                                   hipStream_t st) {
+    if (samples <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_to_channel_major, dim3(tile_grid(samples, n, w)), dim3(256), 0, st, h, hc, samples, n, w,
+                       fq);
     return hipGetLastError();
 }
 
 hipError_t launch_spectral(const SpecArgs& a, hipStream_t st) {
     const int64_t items = a.samples * a.w;
     if (items <= 0) return hipSuccess;
-    const int wpb = a.n <= 2048 ? 4 : 1;
+    const bool small = a.n <= 2048;
+    const int wpb = small ? 4 : 1;
     const int64_t nlogical = (items + wpb - 1) / wpb;
     const unsigned grid = static_cast<unsigned>(8 * ((nlogical + 7) / 8));
-    const size_t lds = static_cast<size_t>(wpb) * a.n * sizeof(float2);
-    if (wpb == 4) {
-        hipLaunchKernelGGL(k_rfft_modes<4>, dim3(grid), dim3(256), lds, st, a, nlogical);
-        hipLaunchKernelGGL(k_mix_irfft<4>, dim3(grid), dim3(256), lds, st, a, nlogical);
-    } else {
-        hipLaunchKernelGGL(k_rfft_modes<1>, dim3(grid), dim3(64), lds, st, a, nlogical);
-        hipLaunchKernelGGL(k_mix_irfft<1>, dim3(grid), dim3(64), lds, st, a, nlogical);
+    // Small grids: the twiddle table (n - 1 values) and 4 waves' buffers in LDS.
+    const size_t lds = (static_cast<size_t>(wpb) * a.n + (small ? a.n : 0)) * sizeof(float2);
+    if (small)
+        hipLaunchKernelGGL((k_rfft_modes<4, true>), dim3(grid), dim3(256), lds, st, a, nlogical);
+    else
+        hipLaunchKernelGGL((k_rfft_modes<1, false>), dim3(grid), dim3(64), lds, st, a, nlogical);
+    if (a.modes > 0) {
+        const dim3 mg(static_cast<unsigned>((a.samples + 3) / 4), static_cast<unsigned>((a.w + 63) / 64),
+                      static_cast<unsigned>(a.modes));
+        hipLaunchKernelGGL(k_spec_mix, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
     }
+    if (small)
+        hipLaunchKernelGGL((k_irfft<4, true>), dim3(grid), dim3(256), lds, st, a, a.spec_mixed, nlogical);
+    else
+        hipLaunchKernelGGL((k_irfft<1, false>), dim3(grid), dim3(64), lds, st, a, a.spec_mixed, nlogical);
     return hipGetLastError();
 }
 
 hipError_t launch_post(const PostArgs& a, hipStream_t st) {
-    const int64_t total = a.M * a.w;
-    if (total <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_post_rt, dim3(grid_for(total, 256, 8)), dim3(256), 0, st, a);
+    if (a.samples <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_post_rt, dim3(tile_grid(a.samples, a.n, a.w)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

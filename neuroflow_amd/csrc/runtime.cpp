@@ -4,9 +4,11 @@
 // (fno.cpp:209-300), optionally build the INT8 local-linear blobs
 // (EnableInt8Gemm, fno.cpp:325-406), and run FNO1d::Forward (fno.cpp:
 // 408-700) with every stage on the GPU:
-//   lift (fp32 Linear) -> L x [input fake-quant, spectral convolution,
-//   local linear (INT8 LinearForwardBatched when dispatched, fp32 Linear
-//   otherwise), act(x1 + fq(x2))] -> proj_q + act -> proj_out.
+//   lift (fp32 Linear) -> channel-major copy (with layer 0's input
+//   fake-quant) -> L x [spectral convolution (channel-major), local linear
+//   (token-major; INT8 LinearForwardBatched when dispatched, fp32 Linear
+//   otherwise), tail act(x1 + fq(x2)) written in both layouts with the next
+//   layer's input fake-quant] -> proj_q + act -> proj_out.
 // The weights live in HBM from creation on; a run allocates nothing once
 // its workspace (grown on demand) fits the shape.
 #include <hip/hip_runtime_api.h>
@@ -280,6 +282,17 @@ int init(nflow_runtime* rt) {
     if (rt->quant_enabled)
         for (const auto& name : weight_names(rt))
             if (int rc = dequantise_weight(rt, name)) return rc;
+    // The spectral weights again, held (modes, in, out) for the channel mix.
+    for (int i = 0; i < rt->n_layers; ++i) {
+        for (const char* part : {"real", "imag"}) {
+            const std::vector<float>& src = rt->w["specs." + std::to_string(i) + ".weights_" + part];
+            std::vector<float> dst(src.size());
+            for (int64_t a = 0; a < w; ++a)
+                for (int64_t o = 0; o < w; ++o)
+                    for (int64_t k = 0; k < m; ++k) dst[(k * w + a) * w + o] = src[(a * w + o) * m + k];
+            rt->w["mix." + std::to_string(i) + "." + part] = std::move(dst);
+        }
+    }
 
     // Per-layer activation quantisation (fno.cpp:482-501, 571-648).
     rt->lq.assign(rt->n_layers, LayerQuant{});
@@ -426,28 +439,37 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
     }
     const float* tw = twiddle_table(rt, static_cast<int>(n_pad));
     if (!tw) return set_error(NFLOW_INTERNAL, "runtime: twiddle upload failed");
-    // Workspace: h, x1, x2 (M x w each) and the kept spectrum.
+    // Workspace: h (token-major), hc (channel-major), x1c, x2 (M x w each)
+    // and the kept spectrum.
     const size_t act_elems = static_cast<size_t>(M) * w;
     const size_t spec_elems = static_cast<size_t>(b) * w * (rt->modes > 0 ? rt->modes : 1) * 2;
     const size_t a64 = (act_elems + 63) & ~size_t(63);
-    if (int rc = ensure_ws(rt, (3 * a64 + spec_elems) * sizeof(float))) return rc;
+    if (int rc = ensure_ws(rt, (4 * a64 + 2 * spec_elems) * sizeof(float))) return rc;
     float* H = static_cast<float*>(rt->ws);
-    float* X1 = H + a64;
-    float* X2 = X1 + a64;
+    float* HC = H + a64;
+    float* X1C = HC + a64;
+    float* X2 = X1C + a64;
     float* SPEC = X2 + a64;
+    float* SPEC2 = SPEC + spec_elems;
+    auto in_fq = [&](int i) {
+        FakeQuant f{0, 1.0f, 0.0f};
+        if (i < rt->n_layers && rt->lq[i].in_fq) f = FakeQuant{1, rt->lq[i].in_scale, static_cast<float>(rt->lq[i].in_zp)};
+        return f;
+    };
 
     LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), H, b, static_cast<int>(n_pad), static_cast<int>(n),
                  static_cast<int>(n), rt->in_ch, w, RT_ACT_NONE};
     if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
+    if (rt->n_layers > 0)
+        if (int rc = launch_check(launch_to_channel_major(H, HC, b, static_cast<int>(n_pad), w, in_fq(0), st),
+                                  "layout change"))
+            return rc;
+    int log2n = 0;
+    while ((int64_t(1) << log2n) < n_pad) ++log2n;
     for (int i = 0; i < rt->n_layers; ++i) {
         const LayerQuant& q = rt->lq[i];
         const std::string si = std::to_string(i);
-        if (q.in_fq)
-            if (int rc = launch_check(launch_fake_quant(H, M * w, q.in_scale, q.in_zp, st), "input fake-quant"))
-                return rc;
-        int log2n = 0;
-        while ((int64_t(1) << log2n) < n_pad) ++log2n;
-        SpecArgs sp{H, SPEC, X1, rt->dw("specs." + si + ".weights_real"), rt->dw("specs." + si + ".weights_imag"),
+        SpecArgs sp{HC, SPEC, SPEC2, X1C, rt->dw("mix." + si + ".real"), rt->dw("mix." + si + ".imag"),
                     tw, tw + 2 * (n_pad > 1 ? n_pad - 1 : 1), b, static_cast<int>(n_pad), log2n, w, rt->modes,
                     1.0f / static_cast<float>(n_pad)};
         if (int rc = launch_check(launch_spectral(sp, st), "spectral convolution")) return rc;
@@ -460,11 +482,12 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
         }
         PostArgs pa{};
         pa.x2 = X2;
-        pa.x1 = X1;
+        pa.x1c = X1C;
         pa.h = H;
-        pa.M = M;
+        pa.hc = HC;
+        pa.samples = b;
+        pa.n = static_cast<int>(n_pad);
         pa.w = w;
-        pa.points = static_cast<int>(n_pad);
         pa.kind = q.x2_kind;
         pa.scale = q.x2_scale;
         pa.zpf = static_cast<float>(q.x2_zp);
@@ -474,13 +497,14 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
         }
         std::memcpy(pa.thr, rt->thr, sizeof(pa.thr));
         pa.act = rt->act;
+        pa.fq_next = in_fq(i + 1);
         if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
     }
     // Trim, proj_q + act, proj_out (fno.cpp:662-698).
-    LinArgs pq{H, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X1, b, static_cast<int>(n), static_cast<int>(n),
+    LinArgs pq{H, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X2, b, static_cast<int>(n), static_cast<int>(n),
                static_cast<int>(n_pad), w, w, rt->act};
     if (int rc = launch_check(launch_linear_ref(pq, st), "proj_q")) return rc;
-    LinArgs po{X1, rt->dw("proj_out.weight"), rt->dw("proj_out.bias"), y, b, static_cast<int>(n), static_cast<int>(n),
+    LinArgs po{X2, rt->dw("proj_out.weight"), rt->dw("proj_out.bias"), y, b, static_cast<int>(n), static_cast<int>(n),
                static_cast<int>(n), w, rt->out_ch, RT_ACT_NONE};
     return launch_check(launch_linear_ref(po, st), "proj_out");
 }

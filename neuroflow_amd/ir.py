@@ -151,3 +151,48 @@ class IR:
             self.close()
         except Exception:
             pass
+
+
+# ---- writing ----------------------------------------------------------------
+
+_CFG_LEN = {1: 7, 2: 7, 3: 8, 4: 7, 5: 8, 6: 8, 7: 8, 8: 8}
+
+
+def write_binary(op_code: int, config: List[int], activation: str, weights: Dict[str, np.ndarray],
+                 qparams: Optional[List[tuple]] = None, version: int = 3) -> bytes:
+    """A NeuroIR binary in the layout ir_native::LoadBinary reads
+    (ir_loader.h:1-40, 95-310, 550-650; written by the reference's
+    neuroflow/ir/export.py): header, config, activation byte, weight records
+    in the given order, and -- when qparams is not None -- the NIRQ block.
+    qparams entries: (0, name, scale, zp) per tensor, (1, name, scales, zps,
+    axis) per channel, (2, name, scales, zps, width) per token, (3, name,
+    scale) FP8."""
+    import struct
+
+    cfg = list(config) + [0] * (_CFG_LEN[op_code] - len(config))
+    out = [b"NIR0", struct.pack("<HBB", version, op_code, 0), struct.pack(f"<{len(cfg)}i", *cfg),
+           struct.pack("<B", 1 if activation == "relu" else 0), b"\x00\x00\x00",
+           struct.pack("<I", len(weights))]
+    for name, arr in weights.items():
+        a = np.ascontiguousarray(arr, np.float32)
+        nb = name.encode()
+        out += [struct.pack("<B", len(nb)), nb, struct.pack("<B", a.ndim), struct.pack(f"<{a.ndim}i", *a.shape),
+                a.tobytes()]
+    if qparams is not None:
+        out += [b"NIRQ", struct.pack("<BI", 1, len(qparams))]
+        for kind, name, *p in qparams:
+            nb = name.encode()
+            out += [struct.pack("<BB", kind, len(nb)), nb]
+            if kind == 0:
+                out.append(struct.pack("<fi", p[0], p[1]))
+            elif kind in (1, 2):
+                scales = np.asarray(p[0], np.float32)
+                zps = np.asarray(p[1], np.int32)
+                out.append(struct.pack("<IB", scales.size, p[2]) if kind == 1 else
+                           struct.pack("<II", scales.size, p[2]))
+                out += [scales.tobytes(), zps.tobytes()]
+            elif kind == 3:
+                out.append(struct.pack("<f", p[0]))
+            else:
+                raise ValueError(f"unknown qparam kind {kind}")
+    return b"".join(out)

@@ -184,6 +184,80 @@ def c5_deeponet_branch(n_samples: int = 4096, sensors: int = 1024, width: int = 
                     samples=n_samples)
 
 
+@dataclass
+class Fno1dModel:
+    name: str
+    ir: bytes                     # NeuroIR binary with its NIRQ block
+    x: np.ndarray                 # (batch, n_points, 1) fp32
+    config: List[int]             # [in_ch, out_ch, width, modes, n_layers, pad_factor]
+    weights: dict = field(default_factory=dict)   # name -> fp32 array, as written into ir
+    qparams: list = field(default_factory=list)   # the NIRQ records, as written into ir
+
+
+def fno1d_model(batch: int = 256, n_points: int = 1024, width: int = 64, modes: int = 16,
+                n_layers: int = 4) -> Fno1dModel:
+    """C2's FNO1d as a whole model (the input fields of C2, width 64, modes
+    16, 4 layers, GELU): lift 1 -> width, the spectral + local-linear layers,
+    proj_q width -> width, proj_out width -> 1.  Weights seeded as the
+    reference's PyTorch modules initialise them (nn.Linear's U(+-1/sqrt(fan_in));
+    spectral weights (1 / width^2) N(0, 1), neuroflow/nn/fno.py:51-56).  The
+    NIRQ block is what calibration exports: per-channel symmetric INT8
+    qparams for every Linear / spectral weight and per-tensor symmetric
+    activation qparams (absmax / 127 over the first two samples, from a
+    float64 pass of the same forward) for lift.output and locs.{i}.output."""
+    from .ir import write_binary
+
+    w = width
+    rng_id = 600
+    weights = {"lift.weight": uniform(rng_id, (w, 1), -1.0, 1.0), "lift.bias": uniform(rng_id + 1, (w,), -1.0, 1.0)}
+    for i in range(n_layers):
+        sc = 1.0 / (w * w)
+        weights[f"specs.{i}.weights_real"] = (sc * normal(rng_id + 10 + 4 * i, (w, w, modes))).astype(np.float32)
+        weights[f"specs.{i}.weights_imag"] = (sc * normal(rng_id + 11 + 4 * i, (w, w, modes))).astype(np.float32)
+        weights[f"locs.{i}.weight"] = kaiming_uniform(rng_id + 12 + 4 * i, w, w)
+        b = 1.0 / math.sqrt(w)
+        weights[f"locs.{i}.bias"] = uniform(rng_id + 13 + 4 * i, (w,), -b, b)
+    b = 1.0 / math.sqrt(w)
+    weights["proj_q.weight"] = kaiming_uniform(rng_id + 90, w, w)
+    weights["proj_q.bias"] = uniform(rng_id + 91, (w,), -b, b)
+    weights["proj_out.weight"] = kaiming_uniform(rng_id + 92, 1, w)
+    weights["proj_out.bias"] = uniform(rng_id + 93, (1,), -b, b)
+    x = sinusoid_fields(200, batch, n_points, 8)[:, :, None].astype(np.float32)
+
+    # Calibration pass (float64, two samples): absmax of each activation.
+    def gelu(z):
+        return 0.5 * z * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (z + 0.044715 * z ** 3)))
+
+    h = x[:2].astype(np.float64) @ weights["lift.weight"].T.astype(np.float64) + weights["lift.bias"]
+    amax = {"lift.output": float(np.abs(h).max())}
+    for i in range(n_layers):
+        spec = np.fft.rfft(h, axis=1)[:, :modes, :]                       # (b, modes, w_in)
+        wc = weights[f"specs.{i}.weights_real"] + 1j * weights[f"specs.{i}.weights_imag"]
+        mixed = np.einsum("bmi,iom->bmo", spec, wc)
+        full = np.zeros((h.shape[0], n_points // 2 + 1, w), np.complex128)
+        full[:, :modes, :] = mixed
+        x1 = np.fft.irfft(full, n=n_points, axis=1)
+        x2 = h @ weights[f"locs.{i}.weight"].T.astype(np.float64) + weights[f"locs.{i}.bias"]
+        amax[f"locs.{i}.output"] = float(np.abs(x2).max())
+        h = gelu(x1 + x2)
+    q = []
+    for name, t in weights.items():
+        if t.ndim == 2:
+            s = np.abs(t).max(axis=1).astype(np.float32) / np.float32(127.0)
+            s[s == 0] = 1.0
+            q.append((1, name, s, np.zeros(t.shape[0], np.int32), 0))
+        elif t.ndim == 3:
+            s = np.abs(t).max(axis=(0, 2)).astype(np.float32) / np.float32(127.0)
+            s[s == 0] = 1.0
+            q.append((1, name, s, np.zeros(t.shape[1], np.int32), 1))
+    for key, a in amax.items():
+        q.append((0, key, float(np.float32(a) / np.float32(127.0)), 0))
+    cfg = [1, 1, w, modes, n_layers, 1]
+    ir = write_binary(1, cfg + [0], "gelu", weights, q)
+    return Fno1dModel(f"FNO1d model, C2 configuration (batch {batch} x {n_points} points, width {w}, "
+                      f"modes {modes}, {n_layers} layers, INT8 local-linear layers, GELU)", ir, x, cfg, weights, q)
+
+
 WORKLOADS = {
     "c1": c1_standalone,
     "c2": c2_fno1d,

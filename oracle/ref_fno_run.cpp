@@ -5,12 +5,20 @@
 // whole FNO1d runs -- and pieces of the layer exposed by crafted weights --
 // with this library.
 //
-//   ref_fno_run <ir> <x.f32> <batch> <n> <in_ch> <out_ch> <y.f32> [int8]
+//   ref_fno_run <ir> <x.f32> <batch> <n> <in_ch> <out_ch> <y.f32> [int8|fp32] [reps] [threads]
 //
-// "int8" calls EnableInt8Gemm() before Run.  Prints "status <code>".
+// "int8" calls EnableInt8Gemm() before Run.  Prints "status <code>".  With
+// reps > 0 it then times `reps` runs of the whole batch, split by samples
+// over `threads` std::threads that each hold their own InferenceRuntime
+// (FNO1d::Forward is single-threaded; one runtime per thread keeps its
+// mutable caches private), and prints "us_per_run <median>".
+#include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <memory>
+#include <string>
+#include <thread>
 #include <vector>
 
 #include "neuroflow/runtime.h"
@@ -19,18 +27,46 @@ int main(int argc, char** argv) {
     if (argc < 8) return 2;
     const int64_t b = std::atoll(argv[3]), n = std::atoll(argv[4]), ci = std::atoll(argv[5]),
                   co = std::atoll(argv[6]);
+    const bool int8 = argc > 8 && std::string(argv[8]) == "int8";
+    const int reps = argc > 9 ? std::atoi(argv[9]) : 0;
+    const int threads = argc > 10 ? std::max(1, std::atoi(argv[10])) : 1;
     std::vector<float> x(static_cast<size_t>(b * n * ci)), y(static_cast<size_t>(b * n * co), 0.0f);
     FILE* fx = std::fopen(argv[2], "rb");
     if (!fx || std::fread(x.data(), sizeof(float), x.size(), fx) != x.size()) return 3;
     std::fclose(fx);
     std::unique_ptr<nflow::InferenceRuntime> rt;
     nflow::Status s = nflow::InferenceRuntime::Create(argv[1], rt);
-    if (s.ok() && argc > 8 && std::string(argv[8]) == "int8") rt->EnableInt8Gemm();
+    if (s.ok() && int8) rt->EnableInt8Gemm();
     if (s.ok()) s = rt->Run(x.data(), {b, n, ci}, y.data(), {b, n, co});
     std::printf("status %d\n", static_cast<int>(s.code()));
     if (!s.ok()) return 0;
     FILE* fy = std::fopen(argv[7], "wb");
     if (!fy || std::fwrite(y.data(), sizeof(float), y.size(), fy) != y.size()) return 4;
     std::fclose(fy);
+    if (reps <= 0) return 0;
+
+    const int T = static_cast<int>(std::min<int64_t>(threads, b));
+    std::vector<std::unique_ptr<nflow::InferenceRuntime>> rts(T);
+    for (int t = 0; t < T; ++t) {
+        if (!nflow::InferenceRuntime::Create(argv[1], rts[t]).ok()) return 5;
+        if (int8) rts[t]->EnableInt8Gemm();
+    }
+    std::vector<double> us;
+    for (int r = 0; r < reps; ++r) {
+        const auto t0 = std::chrono::steady_clock::now();
+        std::vector<std::thread> pool;
+        for (int t = 0; t < T; ++t) {
+            const int64_t s0 = b * t / T, s1 = b * (t + 1) / T;
+            pool.emplace_back([&, t, s0, s1] {
+                if (s1 > s0)
+                    (void)rts[t]->Run(x.data() + s0 * n * ci, {s1 - s0, n, ci}, y.data() + s0 * n * co,
+                                      {s1 - s0, n, co});
+            });
+        }
+        for (auto& th : pool) th.join();
+        us.push_back(std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count());
+    }
+    std::sort(us.begin(), us.end());
+    std::printf("us_per_run %.3f\n", us[us.size() / 2]);
     return 0;
 }

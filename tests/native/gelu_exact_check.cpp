@@ -2,6 +2,7 @@
 // the reference's tanhf comes from): tanhf_fdlibm on every float bit pattern
 // with stride `stride` (1 = all 2^32), and gelu_ref against the reference
 // expression 0.5f*z*(1 + tanhf(c*fma((0.044715f*z)*z, z, z))) with glibc
+// (gelu_ref uses the straight-line tanhf_fdlibm_select, also compared)
 // tanhf and c = sqrtf(2.0f / (float)M_PI).  Prints the mismatch counts.
 // Built with -ffp-contract=off.
 #include <math.h>
@@ -12,7 +13,7 @@
 #include "gelu_exact.h"
 
 static unsigned long long stride_g = 1;
-static unsigned long long bad_tanh[16], bad_gelu[16];
+static unsigned long long bad_tanh[16], bad_gelu[16], bad_sel[16];
 static const int kThreads = 8;
 
 static float gelu_glibc(float z) {
@@ -23,16 +24,19 @@ static float gelu_glibc(float z) {
 
 static void* run(void* arg) {
     const long id = (long)arg;
-    unsigned long long bt = 0, bg = 0;
+    unsigned long long bt = 0, bg = 0, bs = 0;
     for (unsigned long long u = (unsigned long long)id * stride_g; u < (1ull << 32); u += stride_g * kThreads) {
         const float x = nfq::gx_float((uint32_t)u);
         const float a = tanhf(x), b = nfq::tanhf_fdlibm(x);
         if (nfq::gx_bits(a) != nfq::gx_bits(b) && !(isnan(a) && isnan(b))) ++bt;
+        const float c = nfq::tanhf_fdlibm_select(x);
+        if (nfq::gx_bits(a) != nfq::gx_bits(c) && !(isnan(a) && isnan(c))) ++bs;
         const float ga = gelu_glibc(x), gb = nfq::gelu_ref(x);
         if (nfq::gx_bits(ga) != nfq::gx_bits(gb) && !(isnan(ga) && isnan(gb))) ++bg;
     }
     bad_tanh[id] = bt;
     bad_gelu[id] = bg;
+    bad_sel[id] = bs;
     return 0;
 }
 
@@ -40,14 +44,15 @@ int main(int argc, char** argv) {
     stride_g = argc > 1 ? strtoull(argv[1], 0, 10) : 1;
     pthread_t th[kThreads];
     for (long i = 0; i < kThreads; ++i) pthread_create(&th[i], 0, run, (void*)i);
-    unsigned long long bt = 0, bg = 0;
+    unsigned long long bt = 0, bg = 0, bs = 0;
     for (int i = 0; i < kThreads; ++i) {
         pthread_join(th[i], 0);
         bt += bad_tanh[i];
         bg += bad_gelu[i];
+        bs += bad_sel[i];
     }
     const float c_ref = sqrtf(2.0f / (float)3.14159265358979323846);
-    printf("tanh_mismatches %llu gelu_mismatches %llu c_ok %d\n", bt, bg,
+    printf("tanh_mismatches %llu select_mismatches %llu gelu_mismatches %llu c_ok %d\n", bt, bs, bg,
            nfq::gx_bits(c_ref) == nfq::gx_bits(nfq::kGeluC));
     return 0;
 }

@@ -1,7 +1,8 @@
 """The device GELU (neuroflow_amd/csrc/gelu_exact.h, compiled here for the
 host with the library's -ffp-contract=off) against glibc, the libm of the
-reference's tanhf (fno.cpp:41-46): tanhf_fdlibm equal to glibc tanhf, and
-gelu_ref equal to the reference build's expression with glibc tanhf, on
+reference's tanhf (fno.cpp:41-46): tanhf_fdlibm and its straight-line form
+tanhf_fdlibm_select equal to glibc tanhf, and gelu_ref equal to the
+reference build's expression with glibc tanhf, on
 every third float bit pattern (all 2^32 with NFLOW_GELU_STRIDE=1)."""
 import os
 import subprocess
@@ -20,4 +21,4 @@ def test_gelu_exact_matches_glibc(tmp_path):
     out = subprocess.run([str(exe), os.environ.get("NFLOW_GELU_STRIDE", "3")], capture_output=True, text=True,
                          check=True, timeout=600).stdout.split()
     got = dict(zip(out[0::2], out[1::2]))
-    assert got == {"tanh_mismatches": "0", "gelu_mismatches": "0", "c_ok": "1"}, out
+    assert got == {"tanh_mismatches": "0", "select_mismatches": "0", "gelu_mismatches": "0", "c_ok": "1"}, out
