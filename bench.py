@@ -372,6 +372,9 @@ def main():
     N0, K0 = wl.layers[0].W.shape
     if K0 == 64 and N0 == 64:
         kernel = "nfq::k_rows64"
+    elif (wl.layers[0].fmt == "int8" and all(l.W.shape[1] in (128, 256, 512) and l.W.shape[0] % 64 == 0
+                                             for l in wl.layers)):
+        kernel = "nfq::k_token_gemm"    # the whole per-token layer in one launch
     elif K0 % 64 == 0 and K0 >= 128 and wl.layers[0].fmt == "int8":
         kernel = "nfq::k_gemm_pipe"     # after a per-token quantise launch
     else:

@@ -40,7 +40,7 @@ inline unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_p
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// A kernel-selection override read once per process (for A/B comparisons of
+// A kernel-selection override read at each call (for A/B comparisons of
 // two kernels that compute the same bits).
 inline bool getenv_flag(const char* name) {
     const char* v = std::getenv(name);
@@ -78,6 +78,11 @@ void launch_rows(const RowsArgs& a, int act, hipStream_t st);
 bool rows64_ok(const RowsArgs& a);
 template <bool FP8>
 void launch_rows64(const RowsArgs& a, int act, hipStream_t st);
+
+// The one-pass per-token INT8 layer for K = 128 / 256 / 512, N % 64 == 0
+// (token_gemm.hip): quantise into LDS, then the whole N range.
+bool token_gemm_ok(const RowsArgs& a);
+void launch_token_gemm(const RowsArgs& a, int act, hipStream_t st);
 
 // The tiled MFMA GEMM on INT8 codes for K a multiple of 64, K >= 128 (gemm.hip).
 bool gemm_ok(const RowsArgs& a);

@@ -603,6 +603,11 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
         if (post) hipLaunchKernelGGL(k_fno_post, dim3(grid_for(M, 1, 16)), dim3(256), 0, st, C, R, a, activation);
         return check_launch("linear_forward_per_token");
     };
+    // K = 128 .. 512: the one-pass kernel (quantise into LDS, then all of N).
+    if (token_gemm_ok(a) && !getenv_flag("NFLOW_NO_TOKEN_GEMM")) {
+        launch_token_gemm(a, act_x2, st);
+        return finish();
+    }
     // Wide K: quantise into a workspace, then the tiled GEMM (below).
     RowsArgs g = a;
     g.Aq = nullptr;  // the codes go to the workspace, which is 256-byte aligned

@@ -321,3 +321,49 @@ def test_gemm_layer_given_sum_w_not_matching(gpu, M, N, K):
     rows = np.unique(np.concatenate([np.arange(0, M, 17), [M - 1]]))
     ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sw_bad, 1)
     assert _bits_equal(out[rows], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (63, 192, 128), (65, 64, 256), (1000, 768, 256),
+                                   (130, 256, 512), (64, 1024, 512)])
+@pytest.mark.parametrize("form", ["sym", "zp", "zp_sum_off"])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu"])
+def test_token_gemm_layer(gpu, M, N, K, form, act):
+    """The one-pass per-token layer for K = 128 / 256 / 512 (quantise into
+    LDS, then every column block) against LinearForward per row with the
+    row's scale: bit-exact codes' scales and, before GELU, bit-exact outputs;
+    with zero points and a caller's sum_W off the weights' own sums; rows with
+    exact ties, NaN, +-Inf and all zeros; equal to the split path."""
+    import os
+    A = WL.normal(60 + K, (M, K))
+    if M > 8:
+        A[0, 1:] = (np.arange(1, K, dtype=np.float32) % 200 - 100.0) * 0.5   # k + 0.5 ties
+        A[0, 0] = 127.0
+        A[1, :] = 0.0
+        A[2, 5], A[2, 9] = np.nan, np.inf
+        A[3, 7] = -np.inf
+        A[4] = np.nan                                   # every element NaN: scale 1
+        A[5] = 1e-40                                    # subnormal absmax
+        A[6, :] *= 3e-37 / np.abs(A[6]).max()           # normal absmax, subnormal scale
+        A[7, :3] = [1e30, -1e30, 2.5]
+    _, q, s, zps, sw, b = _weights(N, K, 61, zp=form != "sym")
+    sumW = (sw + 3).astype(np.int32) if form == "zp_sum_off" else sw
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sumW))
+    out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
+    code = {"none": 0, "relu": 1, "gelu": 2}[act]
+    ref, sa_ref = O.layer_per_token_i8(A, q, s, zps, b, sumW, code)
+    out = _host(out)
+    assert _bits_equal(_host(sa), sa_ref)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    if act == "gelu":
+        np.testing.assert_allclose(out[fin], ref[fin], rtol=RTOL, atol=ATOL)
+    else:
+        assert _bits_equal(out[fin], ref[fin])
+    os.environ["NFLOW_NO_TOKEN_GEMM"] = "1"
+    try:
+        split = _host(Q.linear_forward_per_token(p, _cu(A), act))
+    finally:
+        del os.environ["NFLOW_NO_TOKEN_GEMM"]
+    keep = ~np.isnan(split)
+    assert np.array_equal(np.isnan(out), ~keep)
+    assert _bits_equal(out[keep], split[keep])
