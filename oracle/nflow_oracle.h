@@ -170,6 +170,13 @@ void orc_cfft(float* a, int n, int inverse);
 /* fft.cpp:72-84 / :86-100. */
 void orc_rfft(const float* x, int n, float* out_complex);
 void orc_irfft(const float* x_complex, int n, float* out);
+/* fft.cpp:101-124 / :126-148: 2-D real FFT of an (H, W) plane to (H, W/2+1)
+ * interleaved bins, and its inverse. */
+void orc_rfft2(const float* x, int H, int W, float* out_complex);
+void orc_irfft2(const float* x_complex, int H, int W, float* out);
+/* fno.cpp:717-771: h, out (bsz, w, H, W); w_real / w_imag (w, w, mh, mw). */
+void orc_spectral_conv2d(const float* h, int bsz, int w, int H, int W, int mh, int mw,
+                         const float* w_real, const float* w_imag, float* out);
 /* fno.cpp:164-207: h, out (bsz, w, n); w_real / w_imag (w, w, modes). */
 void orc_spectral_conv1d(const float* h, int bsz, int w, int n, int modes,
                          const float* w_real, const float* w_imag, float* out);

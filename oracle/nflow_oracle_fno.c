@@ -1,7 +1,8 @@
 /*
  * nflow_oracle_fno.c -- CPU restatement of the pieces of NeuroFlow's FNO1d
- * forward (InferenceRuntime::Run, cpp/src/runtime.cpp:79-101, over
- * FNO1d::Forward, cpp/src/fno.cpp:408-700) that surround the quantised
+ * and FNO2d forwards (InferenceRuntime::Run, cpp/src/runtime.cpp:79-101, over
+ * FNO1d::Forward, cpp/src/fno.cpp:408-700, and FNO2d::Forward, :777-995)
+ * that surround the quantised
  * local-linear layer: the radix-2 FFT (cpp/src/fft.cpp), the spectral
  * convolution, the fp32 Linear loop, the weight and activation fake-quants
  * and the log2 "FP8" snap.  TEST INFRASTRUCTURE ONLY (see nflow_oracle.h).
@@ -147,6 +148,91 @@ void orc_spectral_conv1d(const float* h, int bsz, int w, int n, int modes,
             orc_irfft(O + (size_t)wo * half * 2, n, out + ((size_t)bi * w + wo) * n);
     }
     free(H);
+    free(O);
+}
+
+/* fft.cpp:101-124: the real FFT of each of the H rows (W points each), then
+ * the complex FFT of each of the W/2 + 1 columns; out (H, W/2 + 1)
+ * interleaved complex. */
+void orc_rfft2(const float* x, int H, int W, float* out)
+{
+    const int hw = W / 2 + 1;
+    float* scratch = (float*)malloc(sizeof(float) * 2 * (size_t)H * hw);
+    float* col = (float*)malloc(sizeof(float) * 2 * (size_t)H);
+    for (int i = 0; i < H; ++i) orc_rfft(x + (size_t)i * W, W, scratch + (size_t)i * hw * 2);
+    for (int j = 0; j < hw; ++j) {
+        for (int i = 0; i < H; ++i) {
+            col[2 * i] = scratch[((size_t)i * hw + j) * 2];
+            col[2 * i + 1] = scratch[((size_t)i * hw + j) * 2 + 1];
+        }
+        orc_cfft(col, H, 0);
+        for (int i = 0; i < H; ++i) {
+            out[((size_t)i * hw + j) * 2] = col[2 * i];
+            out[((size_t)i * hw + j) * 2 + 1] = col[2 * i + 1];
+        }
+    }
+    free(col);
+    free(scratch);
+}
+
+/* fft.cpp:126-148: the inverse complex FFT of each of the W/2 + 1 columns
+ * (with its 1/H), then the inverse real FFT of each row (with its 1/W). */
+void orc_irfft2(const float* xc, int H, int W, float* out)
+{
+    const int hw = W / 2 + 1;
+    float* scratch = (float*)malloc(sizeof(float) * 2 * (size_t)H * hw);
+    float* col = (float*)malloc(sizeof(float) * 2 * (size_t)H);
+    for (int j = 0; j < hw; ++j) {
+        for (int i = 0; i < H; ++i) {
+            col[2 * i] = xc[((size_t)i * hw + j) * 2];
+            col[2 * i + 1] = xc[((size_t)i * hw + j) * 2 + 1];
+        }
+        orc_cfft(col, H, 1);
+        for (int i = 0; i < H; ++i) {
+            scratch[((size_t)i * hw + j) * 2] = col[2 * i];
+            scratch[((size_t)i * hw + j) * 2 + 1] = col[2 * i + 1];
+        }
+    }
+    for (int i = 0; i < H; ++i) orc_irfft(scratch + (size_t)i * hw * 2, W, out + (size_t)i * W);
+    free(col);
+    free(scratch);
+}
+
+/* fno.cpp:717-771: h and out (bsz, w, H, W); weights (in=w, out=w, mh, mw);
+ * the output spectrum is zero outside the (mh, mw) corner.  The channel
+ * mix has the 1-D mix's fused terms (the same x86 code in the build). */
+void orc_spectral_conv2d(const float* h, int bsz, int w, int H, int W, int mh, int mw,
+                         const float* w_real, const float* w_imag, float* out)
+{
+    const int hw = W / 2 + 1;
+    const size_t plane = (size_t)H * hw * 2;
+    float* S = (float*)malloc(sizeof(float) * (size_t)w * plane);
+    float* O = (float*)malloc(sizeof(float) * (size_t)w * plane);
+    for (int bi = 0; bi < bsz; ++bi) {
+        memset(O, 0, sizeof(float) * (size_t)w * plane);
+        for (int wi = 0; wi < w; ++wi)
+            orc_rfft2(h + ((size_t)bi * w + wi) * H * W, H, W, S + (size_t)wi * plane);
+        for (int mi = 0; mi < mh; ++mi) {
+            for (int mj = 0; mj < mw; ++mj) {
+                for (int wo = 0; wo < w; ++wo) {
+                    float sr = 0.0f, si = 0.0f;
+                    for (int k = 0; k < w; ++k) {
+                        const float* hv = S + (size_t)k * plane + ((size_t)mi * hw + mj) * 2;
+                        const size_t wix = (((size_t)k * w + wo) * mh + mi) * mw + mj;
+                        const float wr = w_real[wix], wim = w_imag[wix];
+                        sr += fmaf(-wim, hv[1], hv[0] * wr);
+                        si += fmaf(wr, hv[1], hv[0] * wim);
+                    }
+                    float* ov = O + (size_t)wo * plane + ((size_t)mi * hw + mj) * 2;
+                    ov[0] = sr;
+                    ov[1] = si;
+                }
+            }
+        }
+        for (int wo = 0; wo < w; ++wo)
+            orc_irfft2(O + (size_t)wo * plane, H, W, out + ((size_t)bi * w + wo) * H * W);
+    }
+    free(S);
     free(O);
 }
 

@@ -101,6 +101,9 @@ def lib():
         L.orc_rfft.argtypes = [vp, i32, vp]
         L.orc_irfft.argtypes = [vp, i32, vp]
         L.orc_spectral_conv1d.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp]
+        L.orc_rfft2.argtypes = [vp, i32, i32, vp]
+        L.orc_irfft2.argtypes = [vp, i32, i32, vp]
+        L.orc_spectral_conv2d.argtypes = [vp, i32, i32, i32, i32, i32, i32, vp, vp, vp]
         L.orc_linear_f32.argtypes = [vp, vp, vp, i64, i32, i32, vp]
         L.orc_fake_quant_arr.argtypes = [vp, vp, vp, vp, i64]
         L.orc_log2_snap_one.restype = f32
@@ -265,6 +268,35 @@ def spectral_conv1d(h, w_real, w_imag, modes):
     assert wr.shape == (w, w, modes) and wi.shape == wr.shape
     out = np.empty_like(h)
     lib().orc_spectral_conv1d(_ptr(h), b, w, n, modes, _ptr(wr), _ptr(wi), _ptr(out))
+    return out
+
+
+def rfft2(x):
+    """fft.cpp:101-124 on an (H, W) float32 plane: (H, W/2 + 1, 2) bins."""
+    x = _f32(x)
+    H, W = x.shape
+    out = np.empty((H, W // 2 + 1, 2), np.float32)
+    lib().orc_rfft2(_ptr(x), H, W, _ptr(out))
+    return out
+
+
+def irfft2(xc, H, W):
+    """fft.cpp:126-148: (H, W/2 + 1, 2) bins -> (H, W) reals."""
+    xc = _f32(xc)
+    assert xc.shape == (H, W // 2 + 1, 2)
+    out = np.empty((H, W), np.float32)
+    lib().orc_irfft2(_ptr(xc), H, W, _ptr(out))
+    return out
+
+
+def spectral_conv2d(h, w_real, w_imag, mh, mw):
+    """fno.cpp:717-771: h (b, w, H, W) -> (b, w, H, W)."""
+    h = _f32(h)
+    b, w, H, W = h.shape
+    wr, wi = _f32(w_real), _f32(w_imag)
+    assert wr.shape == (w, w, mh, mw) and wi.shape == wr.shape
+    out = np.empty_like(h)
+    lib().orc_spectral_conv2d(_ptr(h), b, w, H, W, mh, mw, _ptr(wr), _ptr(wi), _ptr(out))
     return out
 
 

@@ -3,10 +3,12 @@
 // fft.cpp, tensor.cpp, int8_gemm.cpp, compiled from where they lie) on a raw
 // float32 input, and writes the raw float32 output, so the tests can compare
 // whole FNO1d runs -- and pieces of the layer exposed by crafted weights --
-// with this library.
+// and FNO2d runs -- with this library.
 //
 //   ref_fno_run <ir> <x.f32> <batch> <n> <in_ch> <out_ch> <y.f32> [int8|fp32] [reps] [threads]
 //
+// <n> is the grid: "n" for a 1-D model (shapes (batch, n, ch)) or "HxW" for
+// FNO2d (shapes (batch, H, W, ch)).
 // "int8" calls EnableInt8Gemm() before Run.  Prints "status <code>".  With
 // reps > 0 it then times `reps` runs of the whole batch, split by samples
 // over `threads` std::threads that each hold their own InferenceRuntime
@@ -25,8 +27,23 @@
 
 int main(int argc, char** argv) {
     if (argc < 8) return 2;
-    const int64_t b = std::atoll(argv[3]), n = std::atoll(argv[4]), ci = std::atoll(argv[5]),
-                  co = std::atoll(argv[6]);
+    const int64_t b = std::atoll(argv[3]), ci = std::atoll(argv[5]), co = std::atoll(argv[6]);
+    // Grid: "n" or "HxW".
+    std::vector<int64_t> grid;
+    {
+        const std::string g = argv[4];
+        const size_t xpos = g.find('x');
+        if (xpos == std::string::npos) grid = {std::atoll(g.c_str())};
+        else grid = {std::atoll(g.substr(0, xpos).c_str()), std::atoll(g.substr(xpos + 1).c_str())};
+    }
+    int64_t n = 1;
+    for (int64_t d : grid) n *= d;
+    auto shape = [&](int64_t batch, int64_t ch) {
+        std::vector<int64_t> sh{batch};
+        sh.insert(sh.end(), grid.begin(), grid.end());
+        sh.push_back(ch);
+        return sh;
+    };
     const bool int8 = argc > 8 && std::string(argv[8]) == "int8";
     const int reps = argc > 9 ? std::atoi(argv[9]) : 0;
     const int threads = argc > 10 ? std::max(1, std::atoi(argv[10])) : 1;
@@ -37,7 +54,7 @@ int main(int argc, char** argv) {
     std::unique_ptr<nflow::InferenceRuntime> rt;
     nflow::Status s = nflow::InferenceRuntime::Create(argv[1], rt);
     if (s.ok() && int8) rt->EnableInt8Gemm();
-    if (s.ok()) s = rt->Run(x.data(), {b, n, ci}, y.data(), {b, n, co});
+    if (s.ok()) s = rt->Run(x.data(), shape(b, ci), y.data(), shape(b, co));
     std::printf("status %d\n", static_cast<int>(s.code()));
     if (!s.ok()) return 0;
     FILE* fy = std::fopen(argv[7], "wb");
@@ -59,8 +76,8 @@ int main(int argc, char** argv) {
             const int64_t s0 = b * t / T, s1 = b * (t + 1) / T;
             pool.emplace_back([&, t, s0, s1] {
                 if (s1 > s0)
-                    (void)rts[t]->Run(x.data() + s0 * n * ci, {s1 - s0, n, ci}, y.data() + s0 * n * co,
-                                      {s1 - s0, n, co});
+                    (void)rts[t]->Run(x.data() + s0 * n * ci, shape(s1 - s0, ci), y.data() + s0 * n * co,
+                                      shape(s1 - s0, co));
             });
         }
         for (auto& th : pool) th.join();

@@ -77,6 +77,32 @@ def fno1d_file(weights: Dict[str, np.ndarray], cfg: Sequence[int], qrecords: Lis
     return out
 
 
+def fno2d_weights(rng: np.random.Generator, in_ch: int, out_ch: int, width: int, modes_h: int, modes_w: int,
+                  n_layers: int) -> Dict[str, np.ndarray]:
+    """The FNO2d weight sequence LoadBinary reads (ir_loader.h:298-322)."""
+    f = lambda *s: rng.uniform(-0.5, 0.5, s).astype(np.float32)
+    w = {"lift.weight": f(width, in_ch), "lift.bias": f(width)}
+    for i in range(n_layers):
+        w[f"specs.{i}.weights_real"] = f(width, width, modes_h, modes_w)
+        w[f"specs.{i}.weights_imag"] = f(width, width, modes_h, modes_w)
+        w[f"locs.{i}.weight"] = f(width, width)
+        w[f"locs.{i}.bias"] = f(width)
+    w["proj_q.weight"] = f(width, width)
+    w["proj_q.bias"] = f(width)
+    w["proj_out.weight"] = f(out_ch, width)
+    w["proj_out.bias"] = f(out_ch)
+    return w
+
+
+def fno2d_file(weights: Dict[str, np.ndarray], cfg: Sequence[int], qrecords: List[bytes] | None = None,
+               act: int = 0, version: int = 3) -> bytes:
+    out = header(2, cfg, act, version, len(weights))
+    out += b"".join(weight_record(k, v) for k, v in weights.items())
+    if qrecords is not None:
+        out += nirq(qrecords)
+    return out
+
+
 def symmetric_per_channel(W: np.ndarray, qmax: float = 127.0) -> Tuple[np.ndarray, np.ndarray]:
     s = np.abs(W).max(axis=1).astype(np.float32) / np.float32(qmax)
     s[s == 0] = 1.0
