@@ -32,27 +32,29 @@ extern "C" {
 typedef struct nflow_runtime nflow_runtime;
 
 /* InferenceRuntime::Create (runtime.h:72-73, runtime.cpp:73-77) over
- * LoadNeuroIr + Init (runtime.cpp:15-33): reads the NeuroIR binary, applies
- * the NIRQ weight fake-quant (fno.cpp:209-300), uploads the weights.
- * FileNotFound / ParseError / UnsupportedOp as the reference's loader; an IR
- * of another op than FNO1d is UnsupportedOp. */
+ * LoadNeuroIr + Init (runtime.cpp:15-48): reads the NeuroIR binary, applies
+ * the NIRQ weight fake-quant (fno.cpp:209-300, 997-1020), uploads the
+ * weights.  FileNotFound / ParseError / UnsupportedOp as the reference's
+ * loader; an IR of another op than FNO1d or FNO2d is UnsupportedOp. */
 int nflow_runtime_create(const char* ir_path, nflow_runtime** rt);
 /* The same from an in-memory copy of the file. */
 int nflow_runtime_create_memory(const void* data, size_t bytes, nflow_runtime** rt);
 int nflow_runtime_destroy(nflow_runtime* rt);
 
-/* InferenceRuntime::op() (runtime.h:112): "FNO1d". */
+/* InferenceRuntime::op() (runtime.h:112): "FNO1d" or "FNO2d". */
 const char* nflow_runtime_op(const nflow_runtime* rt);
-/* The FNO1d configuration [in_ch, out_ch, width, modes, n_layers,
- * pad_factor], activation (NFLOW_ACT_RELU / NFLOW_ACT_GELU_TANH) and
+/* The IR's 7-entry configuration block as LoadBinary reads it
+ * (ir_loader.h:131-160): FNO1d [in_ch, out_ch, width, modes, n_layers,
+ * pad_factor, 0], FNO2d [in_ch, out_ch, width, modes_h, modes_w, n_layers,
+ * pad_factor]; the activation (NFLOW_ACT_RELU / NFLOW_ACT_GELU_TANH) and
  * whether the IR carried a NIRQ block.  Any output may be NULL. */
-int nflow_runtime_config(const nflow_runtime* rt, int32_t* config6, int* activation, int* quant_enabled);
+int nflow_runtime_config(const nflow_runtime* rt, int32_t* config7, int* activation, int* quant_enabled);
 
 /* InferenceRuntime::EnableInt8Gemm (runtime.h:99, runtime.cpp:155-166,
  * fno.cpp:360-406): builds and uploads the INT8 blob of every locs.{i}
  * weight with per-channel qparams; those layers then run as the INT8
  * LinearForwardBatched when LinearDispatchTryInt8 would take it
- * (fno.cpp:125-159). */
+ * (fno.cpp:125-159).  A no-op for FNO2d, as in the reference. */
 int nflow_runtime_enable_int8_gemm(nflow_runtime* rt);
 /* InferenceRuntime::IsInt8GemmEnabled (runtime.h:103, runtime.cpp:168-171). */
 int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled);
@@ -60,9 +62,10 @@ int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled);
 int nflow_runtime_layer_dispatch(const nflow_runtime* rt, int layer_index, int* uses_int8);
 
 /* InferenceRuntime::Run (runtime.h:77-78, runtime.cpp:79-94) on HOST buffers:
- * x (batch, n, in_ch), y (batch, n, out_ch), float32, C-contiguous; copies
+ * x (batch, n, in_ch), y (batch, n, out_ch) for FNO1d, x (batch, H, W,
+ * in_ch), y (batch, H, W, out_ch) for FNO2d; float32, C-contiguous; copies
  * in, runs, copies out, synchronises.  Shape checks and their codes as
- * FNO1d::Forward (fno.cpp:409-425). */
+ * FNO1d::Forward (fno.cpp:409-425) / FNO2d::Forward (fno.cpp:778-795). */
 int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape, int x_ndim, float* y,
                       const int64_t* y_shape, int y_ndim);
 /* The same on DEVICE buffers, enqueued on `stream` without synchronising. */

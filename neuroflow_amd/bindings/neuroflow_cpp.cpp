@@ -12,8 +12,8 @@
 //                           y_ptr, y_shape, stream=0) on device pointers
 //   fp8_e4m3_fake_quant(in, scale), fp8_e4m3_to_bits(in), fp8_e4m3_from_bits(in)
 //
-// The runtime serves FNO1d (include/nflow_runtime.h); creating it from an IR
-// of another op fails with the runtime's UnsupportedOp message.
+// The runtime serves FNO1d and FNO2d (include/nflow_runtime.h); creating it
+// from an IR of another op fails with the runtime's UnsupportedOp message.
 #include <hip/hip_runtime_api.h>
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
@@ -72,8 +72,9 @@ std::unique_ptr<nflow::InferenceRuntime> create(const std::string& path) {
 // infer_arrays / infer: y shape = x shape with the last dim out_channels.
 py::array_t<float> run_arrays(nflow::InferenceRuntime& rt, const F32Array& x) {
     py::buffer_info xb = x.request();
-    if (xb.ndim != 3) throw std::runtime_error("input rank mismatch for op " + rt.op());
-    int32_t cfg[6] = {};
+    if (static_cast<size_t>(xb.ndim) != expected_rank(rt.op()))
+        throw std::runtime_error("input rank mismatch for op " + rt.op());
+    int32_t cfg[7] = {};
     (void)nflow_runtime_config(rt.handle(), cfg, nullptr, nullptr);
     std::vector<int64_t> ys = shape_of(xb);
     ys.back() = cfg[1];
@@ -110,7 +111,7 @@ py::array_t<Out> on_device(const py::array_t<In, py::array::c_style | py::array:
 }  // namespace
 
 PYBIND11_MODULE(neuroflow_cpp, m) {
-    m.doc() = "NeuroFlow runtime on the MI355X - FNO1d inference with the quantised GEMM on the GPU";
+    m.doc() = "NeuroFlow runtime on the MI355X - FNO1d / FNO2d inference on the GPU";
 
     m.def(
         "infer",
@@ -175,7 +176,7 @@ PYBIND11_MODULE(neuroflow_cpp, m) {
                 if (!s.ok()) throw std::runtime_error("Run failed: " + s.message());
             },
             py::arg("x"), py::arg("y"),
-            "Run FNO1d inference.  x and y are pre-allocated float32 numpy arrays with the "
+            "Run FNO1d / FNO2d inference.  x and y are pre-allocated float32 numpy arrays with the "
             "expected input/output shapes.")
         .def(
             "run_device",
@@ -198,7 +199,7 @@ PYBIND11_MODULE(neuroflow_cpp, m) {
             const std::string op = ir_op(model_path);
             if (op != "DeepONet")
                 throw std::runtime_error("infer_deeponet_arrays: model op is " + op + ", not DeepONet");
-            create(model_path);  // throws: the device runtime serves FNO1d
+            create(model_path);  // throws: the device runtime serves FNO1d and FNO2d
             return py::array_t<float>();
         },
         py::arg("model_path"), py::arg("u"), py::arg("y"),

@@ -1,14 +1,15 @@
-// fno1d.h -- launchers of the FNO1d runtime's device kernels (fno1d.hip),
-// called by the host runtime (runtime.cpp).  Every launcher is stream-ordered
-// and returns hipError_t of the launch.
+// fno_rt.h -- launchers of the FNO1d / FNO2d runtime's device kernels
+// (fno_rt.hip), called by the host runtime (runtime.cpp).  Every launcher is
+// stream-ordered and returns hipError_t of the launch.
 //
 // Layouts: the local-linear layers read and write token-major activations,
 // (samples, points, width) with width contiguous; the spectral convolution
 // reads and writes channel-major ones, (samples, width, points) with points
-// contiguous -- the reference's layout (fno.cpp:437-445, 523-556).  The layer
-// tail writes the new activation in both.  Only the layout differs from the
-// reference: every element is computed by the same float operations as its
-// x86 build.
+// contiguous -- the reference's layout (fno.cpp:437-445, 523-556; for FNO2d
+// the points are the H x W grid, row-major, fno.cpp:855-865, 906-932).  The
+// layer tail writes the new activation in both.  Only the layout differs
+// from the reference: every element is computed by the same float
+// operations as its x86 build.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -44,11 +45,14 @@ struct LinArgs {
 };
 hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st);
 
-// The INT8 fake-quant of an activation (fno.cpp:488-501), optional.
+// An activation fake-quant: on = 0 none, 1 the INT8 per-tensor round trip
+// (fno.cpp:488-501, 637-646, 830-842), 3 the log2 "FP8" snap (fno.cpp:579-606,
+// 813-829) with its exponent step points in thr (see PostArgs).
 struct FakeQuant {
     int on;
     float scale;
     float zpf;
+    float thr[15];
 };
 
 // Token-major h (samples, n, w) to channel-major hc (samples, w, n), with the
@@ -77,8 +81,47 @@ struct SpecArgs {
     int w;
     int modes;
     float inv_n;
+    // Inverse FFT only: the value of the bins modes .. n/2 of item r is
+    // fill[r % fill_period] (their mirrors its conjugate); null: (0, 0).
+    const float2* fill;
+    int fill_period;
 };
 hipError_t launch_spectral(const SpecArgs& a, hipStream_t st);
+
+// The pieces of launch_spectral one at a time, for the 2-D convolution
+// (fno.cpp:717-771 over fft.cpp:101-148).  Items are samples * w rows of n
+// points (hc / x1c), each with `modes` kept bins (spec / spec_mixed).
+hipError_t launch_rfft_rows(const SpecArgs& a, hipStream_t st);   // hc -> spec
+hipError_t launch_spec_mix(const SpecArgs& a, hipStream_t st);    // spec -> spec_mixed
+hipError_t launch_irfft_rows(const SpecArgs& a, hipStream_t st);  // spec_mixed (+ fill) -> x1c
+
+// Column FFTs of the 2-D transform: `planes` planes of complex values with
+// row stride mw (mw columns, j < mw); a radix-2 complex FFT of length h
+// (fft.cpp:48-68) down each column.  Forward: in (planes, h, mw) -> rows
+// 0 .. mh - 1 of the result to out (planes, mh, mw).  Inverse: in
+// (planes, mh, mw), rows mh .. h - 1 taken as (0, 0) -> out (planes, h, mw),
+// scaled by 1/h.  tw: the forward or inverse stage twiddles of length h.
+struct ColArgs {
+    const float* in;
+    float* out;
+    const float* tw;
+    int64_t planes;
+    int h;
+    int log2h;
+    int mw;
+    int mh;
+    float inv_h;
+};
+hipError_t launch_cfft_cols(const ColArgs& a, bool inverse, hipStream_t st);
+
+// Token-major (samples, h, w, c) <-> (samples, hp, wp, c): pad copies the
+// grid into the top-left corner of the larger one and zeroes the rest
+// (fno.cpp:867-891); trim copies the corner back out (fno.cpp:946-964).
+hipError_t launch_pad2d(const float* src, float* dst, int64_t samples, int h, int w, int hp, int wp, int c,
+                        bool trim, hipStream_t st);
+
+// y[i] = act(fq(y[i])) in place over n elements (fno.cpp:980-993).
+hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t st);
 
 // The layer tail h = act(x1 + fq(x2)) (fno.cpp:558-660) from token-major x2
 // and channel-major x1c, written to token-major h and channel-major hc, with

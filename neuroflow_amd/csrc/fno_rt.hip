@@ -1,7 +1,8 @@
-// fno1d.hip -- device kernels of the FNO1d runtime around the quantised
-// local-linear layer: the fp32 Linear of the lift / projection / fallback
-// layers, the input fake-quant, the spectral convolution (radix-2 FFT,
-// channel mix, inverse FFT) and the layer tail act(x1 + fq(x2)).
+// fno_rt.hip -- device kernels of the FNO1d / FNO2d runtime around the
+// quantised local-linear layer: the fp32 Linear of the lift / projection /
+// fallback layers, the activation fake-quants, the spectral convolution
+// (radix-2 FFTs along rows and, in 2-D, columns; channel mix; inverse FFTs)
+// and the layer tail act(x1 + fq(x2)).
 //
 // Every element is computed by the float operations of the reference build
 // (cpp/src/fno.cpp and fft.cpp compiled by g++ -O3 -mfma): products the
@@ -13,7 +14,7 @@
 #include <algorithm>
 
 #include "common.h"
-#include "fno1d.h"
+#include "fno_rt.h"
 #include "gelu_exact.h"
 #include "launch.h"
 
@@ -207,8 +208,34 @@ __device__ __forceinline__ bool tile_of(int64_t id, int64_t samples, int n, int 
     return true;
 }
 
-__device__ __forceinline__ float apply_fq(float v, FakeQuant q) {
-    return q.on ? x2_fake_quant(v, q.scale, q.zpf) : v;
+// fno.cpp:579-606 with the exponent e = int(std::round(log2|v| * 8) / 8)
+// read off the step points of the reference's libm (thr: the smallest float
+// of each exponent from -5 to 9, computed on the host with that libm):
+// e = -6 + #{thr <= |v|} for 2^-6 <= |v| <= FLT_MAX; NaN and Inf give
+// ldexp(1, INT_MIN) = 0; 2^e for e >= 9 is capped at 448.
+__device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
+    const float v = x / s;
+    const float av = fabsf(v);
+    const float sign = v < 0.0f ? -1.0f : 1.0f;
+    float qv;
+    if (av < 0.015625f) {
+        qv = av;
+    } else if (!(av <= 0x1.fffffep+127f)) {
+        qv = 0.0f;
+    } else {
+        int e = -6;
+#pragma unroll
+        for (int j = 0; j < 15; ++j) e += av >= thr[j] ? 1 : 0;
+        qv = e >= 9 ? 448.0f : __builtin_bit_cast(float, static_cast<uint32_t>(127 + e) << 23);
+    }
+    const float clamped = (448.0f < qv) ? 448.0f : qv;
+    return (sign * clamped) * s;
+}
+
+__device__ __forceinline__ float apply_fq(float v, const FakeQuant& q) {
+    if (q.on == 1) return x2_fake_quant(v, q.scale, q.zpf);
+    if (q.on == 3) return log2_snap(v, q.scale, q.thr);
+    return v;
 }
 
 __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, int64_t samples, int n, int w,
@@ -221,7 +248,7 @@ __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, i
             if (t < n && c < w) {
                 const int64_t o = (tl.s * n + t) * w + c;
                 const float v = apply_fq(h[o], fq);
-                if (fq.on) h[o] = v;
+                if (fq.on != 0) h[o] = v;
                 tile[cr][tr] = v;
             }
         }
@@ -255,10 +282,12 @@ __device__ __forceinline__ float2 cmul_ref(float2 x, float2 w) {
 // is tw[h - 1 + kk + (e mod 2^st) h0].
 //   SRC 0: LDS buf; 1: the channel's real input, bit-reversed on load;
 //          2: the mixed spectrum, bins above n/2 the conjugates of those
-//             below (fft.cpp:86-96), bins >= modes zero ((0, 0) below n/2,
-//             their mirrors (0, -0));
+//             below (fft.cpp:86-96), bins >= modes the fill value below
+//             n/2 and its conjugate above ((0, 0) and (0, -0) in 1-D);
+//          3: a strided complex column, rows >= src_rows (0, 0);
 //   DST 0: LDS buf; 1: bins < modes to the kept spectrum; 2: real parts
-//          times 1/n to the channel's output.
+//          times 1/n to the channel's output; 3: rows < dst_rows to a
+//          strided complex column, times 1/n when `scale`.
 struct FftIo {
     float2* buf;
     const float2* tw;
@@ -270,6 +299,10 @@ struct FftIo {
     int log2n;
     int modes;
     float inv_n;
+    float fill_re, fill_im;
+    int src_stride, src_rows;
+    int dst_stride, dst_rows;
+    bool scale;
 };
 
 template <int SRC>
@@ -280,15 +313,20 @@ __device__ __forceinline__ float2 fft_load(const FftIo& io, int e) {
         const int k = bit_rev(e, io.log2n);
         if constexpr (SRC == 1) {
             return make_float2(io.src_real[k], 0.0f);
-        } else {
+        } else if constexpr (SRC == 2) {
             const int nh = io.n >> 1;
-            if (k <= nh) return k < io.modes ? io.src_spec[k] : make_float2(0.0f, 0.0f);
+            if (k <= nh) {
+                if (k < io.modes) return io.src_spec[k];
+                return make_float2(io.fill_re, io.fill_im);
+            }
             const int kk = io.n - k;
             if (kk < io.modes) {
                 const float2 v = io.src_spec[kk];
                 return make_float2(v.x, -v.y);
             }
-            return make_float2(0.0f, -0.0f);
+            return make_float2(io.fill_re, -io.fill_im);
+        } else {
+            return k < io.src_rows ? io.src_spec[static_cast<int64_t>(k) * io.src_stride] : make_float2(0.0f, 0.0f);
         }
     }
 }
@@ -299,8 +337,11 @@ __device__ __forceinline__ void fft_store(const FftIo& io, int e, float2 v) {
         io.buf[e] = v;
     } else if constexpr (DST == 1) {
         if (e < io.modes) io.dst_spec[e] = v;
-    } else {
+    } else if constexpr (DST == 2) {
         io.dst_real[e] = v.x * io.inv_n;
+    } else {
+        if (e < io.dst_rows)
+            io.dst_spec[static_cast<int64_t>(e) * io.dst_stride] = io.scale ? make_float2(v.x * io.inv_n, v.y * io.inv_n) : v;
     }
 }
 
@@ -338,19 +379,22 @@ template <int P, int SRC>
 __device__ __forceinline__ void fft_pass_to(const FftIo& io, int h0, int lane, bool last, int dst_last) {
     if (!last) fft_pass<P, SRC, 0>(io, h0, lane);
     else if (dst_last == 1) fft_pass<P, SRC, 1>(io, h0, lane);
-    else fft_pass<P, SRC, 2>(io, h0, lane);
+    else if (dst_last == 2) fft_pass<P, SRC, 2>(io, h0, lane);
+    else fft_pass<P, SRC, 3>(io, h0, lane);
 }
 
 // The whole transform of one channel by one wave: the first pass reads the
 // source (SRC), the last writes the destination (dst_last), the others go
 // through the wave's LDS buffer.
 template <int SRC>
-__device__ void fft_run(const FftIo& io, int lane, int dst_last) {
+__device__ __forceinline__ void fft_run(const FftIo& io, int lane, int dst_last) {
     const int L = io.log2n;
     if (L == 0) {
+        if (lane != 0) return;
         const float2 v = fft_load<SRC>(io, 0);
         if (dst_last == 1) fft_store<1>(io, 0, v);
-        else fft_store<2>(io, 0, v);
+        else if (dst_last == 2) fft_store<2>(io, 0, v);
+        else fft_store<3>(io, 0, v);
         return;
     }
     int done = 0, h0 = 1;
@@ -452,36 +496,48 @@ __global__ __launch_bounds__(64 * WPB) void k_irfft(SpecArgs a, const float* spe
     io.log2n = a.log2n;
     io.modes = a.modes;
     io.inv_n = a.inv_n;
+    if (a.fill) {
+        const float2 f = a.fill[item % a.fill_period];
+        io.fill_re = f.x;
+        io.fill_im = f.y;
+    }
     fft_run<2>(io, lane, 2);
+}
+
+// Column FFT (fft.cpp:48-68 down column j of a plane, fft.cpp:111-122 /
+// :131-141): item = plane * mw + j.
+template <int WPB, bool TWL, bool INV>
+__global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogical) {
+    extern __shared__ float2 fsm[];
+    const int n = a.h;
+    const float2* tw = block_twiddles<TWL>(fsm, a.tw, n);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int64_t lb = xcd_block(nlogical);
+    if (lb < 0) return;
+    const int64_t item = lb * WPB + wid;
+    if (item >= a.planes * a.mw) return;
+    const int64_t plane = item / a.mw;
+    const int j = static_cast<int>(item % a.mw);
+    const int in_rows = INV ? a.mh : a.h, out_rows = INV ? a.h : a.mh;
+    FftIo io{};
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.tw = tw;
+    io.src_spec = reinterpret_cast<const float2*>(a.in) + plane * in_rows * a.mw + j;
+    io.src_stride = a.mw;
+    io.src_rows = in_rows;
+    io.dst_spec = reinterpret_cast<float2*>(a.out) + plane * out_rows * a.mw + j;
+    io.dst_stride = a.mw;
+    io.dst_rows = out_rows;
+    io.n = n;
+    io.log2n = a.log2h;
+    io.inv_n = a.inv_h;
+    io.scale = INV;
+    fft_run<3>(io, lane, 3);
 }
 
 // ---------------------------------------------------------------------------
 // Layer tail.
 // ---------------------------------------------------------------------------
-
-// fno.cpp:579-606 with the exponent e = int(std::round(log2|v| * 8) / 8)
-// read off the step points of the reference's libm (thr: the smallest float
-// of each exponent from -5 to 9, computed on the host with that libm):
-// e = -6 + #{thr <= |v|} for 2^-6 <= |v| <= FLT_MAX; NaN and Inf give
-// ldexp(1, INT_MIN) = 0; 2^e for e >= 9 is capped at 448.
-__device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
-    const float v = x / s;
-    const float av = fabsf(v);
-    const float sign = v < 0.0f ? -1.0f : 1.0f;
-    float qv;
-    if (av < 0.015625f) {
-        qv = av;
-    } else if (!(av <= 0x1.fffffep+127f)) {
-        qv = 0.0f;
-    } else {
-        int e = -6;
-#pragma unroll
-        for (int j = 0; j < 15; ++j) e += av >= thr[j] ? 1 : 0;
-        qv = e >= 9 ? 448.0f : __builtin_bit_cast(float, static_cast<uint32_t>(127 + e) << 23);
-    }
-    const float clamped = (448.0f < qv) ? 448.0f : qv;
-    return (sign * clamped) * s;
-}
 
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
     __shared__ float tx1[64][65];  // x1, then (in place, same thread) the new h
@@ -521,6 +577,36 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// FNO2d padding and the projection fake-quants.
+// ---------------------------------------------------------------------------
+
+// One thread per element of the larger grid (samples, hp, wp, c).
+__global__ __launch_bounds__(256) void k_pad2d(const float* src, float* dst, int64_t samples, int h, int w, int hp,
+                                               int wp, int c, int trim) {
+    const int64_t total = samples * hp * wp * c;
+    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+        const int ch = static_cast<int>(i % c);
+        const int64_t p = i / c;
+        const int x = static_cast<int>(p % wp);
+        const int64_t q = p / wp;
+        const int y = static_cast<int>(q % hp);
+        const int64_t s = q / hp;
+        const bool in = y < h && x < w;
+        const int64_t small = ((s * h + y) * w + x) * c + ch;
+        if (trim) {
+            if (in) dst[small] = src[i];
+        } else {
+            dst[i] = in ? src[small] : 0.0f;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_fq_act(float* y, int64_t n, FakeQuant fq, int act) {
+    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+        y[i] = rt_activate(apply_fq(y[i], fq), act);
+}
+
+// ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
 
@@ -551,28 +637,91 @@ hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, 
     return hipGetLastError();
 }
 
-hipError_t launch_spectral(const SpecArgs& a, hipStream_t st) {
+// One wave per FFT of n points: 4 waves per block with the twiddle table
+// (n - 1 values) in LDS when n <= 2048, else one wave reading it from L2.
+// Blocks are dealt to the 8 XCDs in contiguous logical ranges (xcd_block).
+struct FftLaunch {
+    bool small;
+    int64_t nlogical;
+    unsigned grid;
+    size_t lds;
+};
+static FftLaunch fft_launch(int64_t items, int n) {
+    FftLaunch f{};
+    f.small = n <= 2048;
+    const int wpb = f.small ? 4 : 1;
+    f.nlogical = (items + wpb - 1) / wpb;
+    f.grid = static_cast<unsigned>(8 * ((f.nlogical + 7) / 8));
+    f.lds = (static_cast<size_t>(wpb) * n + (f.small ? n : 0)) * sizeof(float2);
+    return f;
+}
+
+hipError_t launch_rfft_rows(const SpecArgs& a, hipStream_t st) {
     const int64_t items = a.samples * a.w;
     if (items <= 0) return hipSuccess;
-    const bool small = a.n <= 2048;
-    const int wpb = small ? 4 : 1;
-    const int64_t nlogical = (items + wpb - 1) / wpb;
-    const unsigned grid = static_cast<unsigned>(8 * ((nlogical + 7) / 8));
-    // Small grids: the twiddle table (n - 1 values) and 4 waves' buffers in LDS.
-    const size_t lds = (static_cast<size_t>(wpb) * a.n + (small ? a.n : 0)) * sizeof(float2);
-    if (small)
-        hipLaunchKernelGGL((k_rfft_modes<4, true>), dim3(grid), dim3(256), lds, st, a, nlogical);
+    const FftLaunch f = fft_launch(items, a.n);
+    if (f.small)
+        hipLaunchKernelGGL((k_rfft_modes<4, true>), dim3(f.grid), dim3(256), f.lds, st, a, f.nlogical);
     else
-        hipLaunchKernelGGL((k_rfft_modes<1, false>), dim3(grid), dim3(64), lds, st, a, nlogical);
-    if (a.modes > 0) {
-        const dim3 mg(static_cast<unsigned>((a.samples + 3) / 4), static_cast<unsigned>((a.w + 63) / 64),
-                      static_cast<unsigned>(a.modes));
-        hipLaunchKernelGGL(k_spec_mix, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
+        hipLaunchKernelGGL((k_rfft_modes<1, false>), dim3(f.grid), dim3(64), f.lds, st, a, f.nlogical);
+    return hipGetLastError();
+}
+
+hipError_t launch_spec_mix(const SpecArgs& a, hipStream_t st) {
+    if (a.samples <= 0 || a.w <= 0 || a.modes <= 0) return hipSuccess;
+    const dim3 mg(static_cast<unsigned>((a.samples + 3) / 4), static_cast<unsigned>((a.w + 63) / 64),
+                  static_cast<unsigned>(a.modes));
+    hipLaunchKernelGGL(k_spec_mix, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
+    return hipGetLastError();
+}
+
+hipError_t launch_irfft_rows(const SpecArgs& a, hipStream_t st) {
+    const int64_t items = a.samples * a.w;
+    if (items <= 0) return hipSuccess;
+    const FftLaunch f = fft_launch(items, a.n);
+    if (f.small)
+        hipLaunchKernelGGL((k_irfft<4, true>), dim3(f.grid), dim3(256), f.lds, st, a, a.spec_mixed, f.nlogical);
+    else
+        hipLaunchKernelGGL((k_irfft<1, false>), dim3(f.grid), dim3(64), f.lds, st, a, a.spec_mixed, f.nlogical);
+    return hipGetLastError();
+}
+
+hipError_t launch_spectral(const SpecArgs& a, hipStream_t st) {
+    if (hipError_t e = launch_rfft_rows(a, st)) return e;
+    if (hipError_t e = launch_spec_mix(a, st)) return e;
+    return launch_irfft_rows(a, st);
+}
+
+hipError_t launch_cfft_cols(const ColArgs& a, bool inverse, hipStream_t st) {
+    const int64_t items = a.planes * a.mw;
+    if (items <= 0) return hipSuccess;
+    const FftLaunch f = fft_launch(items, a.h);
+    if (inverse) {
+        if (f.small)
+            hipLaunchKernelGGL((k_cfft_cols<4, true, true>), dim3(f.grid), dim3(256), f.lds, st, a, f.nlogical);
+        else
+            hipLaunchKernelGGL((k_cfft_cols<1, false, true>), dim3(f.grid), dim3(64), f.lds, st, a, f.nlogical);
+    } else {
+        if (f.small)
+            hipLaunchKernelGGL((k_cfft_cols<4, true, false>), dim3(f.grid), dim3(256), f.lds, st, a, f.nlogical);
+        else
+            hipLaunchKernelGGL((k_cfft_cols<1, false, false>), dim3(f.grid), dim3(64), f.lds, st, a, f.nlogical);
     }
-    if (small)
-        hipLaunchKernelGGL((k_irfft<4, true>), dim3(grid), dim3(256), lds, st, a, a.spec_mixed, nlogical);
-    else
-        hipLaunchKernelGGL((k_irfft<1, false>), dim3(grid), dim3(64), lds, st, a, a.spec_mixed, nlogical);
+    return hipGetLastError();
+}
+
+hipError_t launch_pad2d(const float* src, float* dst, int64_t samples, int h, int w, int hp, int wp, int c,
+                        bool trim, hipStream_t st) {
+    const int64_t total = samples * hp * wp * c;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_pad2d, dim3(grid_for(total, 256, 8)), dim3(256), 0, st, src, dst, samples, h, w, hp, wp, c,
+                       trim ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t st) {
+    if (n <= 0 || (fq.on == 0 && act == RT_ACT_NONE)) return hipSuccess;
+    hipLaunchKernelGGL(k_fq_act, dim3(grid_for(n, 256, 8)), dim3(256), 0, st, y, n, fq, act);
     return hipGetLastError();
 }
 

@@ -1,14 +1,20 @@
-// runtime.cpp -- nflow::InferenceRuntime for FNO1d on the device
+// runtime.cpp -- nflow::InferenceRuntime for FNO1d and FNO2d on the device
 // (cpp/src/runtime.cpp:15-101, 150-173, cpp/include/neuroflow/runtime.h:
 // 64-121): load a NeuroIR binary, apply the NIRQ weight fake-quant
-// (fno.cpp:209-300), optionally build the INT8 local-linear blobs
-// (EnableInt8Gemm, fno.cpp:325-406), and run FNO1d::Forward (fno.cpp:
-// 408-700) with every stage on the GPU:
-//   lift (fp32 Linear) -> channel-major copy (with layer 0's input
+// (fno.cpp:209-300, 997-1020), optionally build the INT8 local-linear blobs
+// (EnableInt8Gemm, fno.cpp:325-406; FNO1d only, as in the reference), and
+// run FNO1d::Forward (fno.cpp:408-700) or FNO2d::Forward (fno.cpp:777-995)
+// with every stage on the GPU:
+//   FNO1d: lift (fp32 Linear) -> channel-major copy (with layer 0's input
 //   fake-quant) -> L x [spectral convolution (channel-major), local linear
 //   (token-major; INT8 LinearForwardBatched when dispatched, fp32 Linear
 //   otherwise), tail act(x1 + fq(x2)) written in both layouts with the next
 //   layer's input fake-quant] -> proj_q + act -> proj_out.
+//   FNO2d: lift (+ lift.output fake-quant) -> zero padding -> channel-major
+//   copy -> L x [row FFTs, column FFTs of the kept columns, channel mix of
+//   the (modes_h, modes_w) corner, inverse column FFTs, inverse row FFTs;
+//   fp32 local linear; tail act(x1 + fq(x2))] -> trim -> proj_q + fake-quant
+//   + act -> proj_out + fake-quant.
 // The weights live in HBM from creation on; a run allocates nothing once
 // its workspace (grown on demand) fits the shape.
 #include <hip/hip_runtime_api.h>
@@ -22,7 +28,7 @@
 #include <string>
 #include <vector>
 
-#include "fno1d.h"
+#include "fno_rt.h"
 #include "nflow_quant.h"
 #include "nflow_runtime.h"
 #include "status.h"
@@ -122,6 +128,34 @@ void twiddles(int n, bool inverse, std::vector<float>& out) {
 
 bool is_pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
 
+// The inverse complex FFT of n zeros (fft.cpp:48-68 with the table above):
+// the reference's inverse 2-D transform runs it down every column it does
+// not mix (fft.cpp:131-141), and its products can carry -0.0f, which the
+// row transforms then read as those columns' bins.  out: n complex values.
+void zero_column_ifft(int n, const std::vector<float>& tw_inv, std::vector<float>& out) {
+    out.assign(2 * static_cast<size_t>(n), 0.0f);
+    for (int len = 2; len <= n; len <<= 1) {
+        const int half = len / 2;
+        for (int i = 0; i < n; i += len) {
+            for (int k = 0; k < half; ++k) {
+                float* u = out.data() + 2 * static_cast<size_t>(i + k);
+                float* v = out.data() + 2 * static_cast<size_t>(i + k + half);
+                const float wr = tw_inv[2 * static_cast<size_t>(half - 1 + k)];
+                const float wi = tw_inv[2 * static_cast<size_t>(half - 1 + k) + 1];
+                const float tr = std::fma(v[0], wr, -(v[1] * wi));
+                const float ti = std::fma(v[0], wi, v[1] * wr);
+                const float ur = u[0], ui = u[1];
+                u[0] = ur + tr;
+                u[1] = ui + ti;
+                v[0] = ur - tr;
+                v[1] = ui - ti;
+            }
+        }
+    }
+    const float inv = 1.0f / static_cast<float>(n);
+    for (float& f : out) f *= inv;
+}
+
 }  // namespace
 }  // namespace nfq
 
@@ -130,10 +164,15 @@ using namespace nfq;
 struct nflow_runtime {
     std::string op;
     int device = 0;
+    int32_t cfg[7] = {};              // the IR's configuration block
+    bool fno2d = false;
     int in_ch = 0, out_ch = 0, width = 0, modes = 0, n_layers = 0, pad_factor = 1;
+    int modes_h = 0, modes_w = 0;     // FNO2d (modes = modes_h * modes_w there)
     int act = RT_ACT_GELU;
     bool quant_enabled = false;
     bool int8_enabled = false;
+    // FNO2d's fake-quants outside the layers (lift / proj_q / proj_out .output).
+    FakeQuant fq_lift{}, fq_projq{}, fq_projout{};
 
     // Host copies of the IR data the runtime needs after creation.
     nflow_ir* ir = nullptr;
@@ -146,8 +185,10 @@ struct nflow_runtime {
     std::map<std::string, size_t> off;  // float offsets into dblock
     std::vector<nflow_layer*> int8_layers;
 
-    // Device twiddles per grid length, workspace grown on demand.
+    // Device twiddles per grid length, the zero-column pattern per column
+    // length (FNO2d), workspace grown on demand.
     std::map<int, float*> tw;
+    std::map<int, float*> zfill;
     void* ws = nullptr;
     size_t ws_bytes = 0;
 
@@ -166,6 +207,7 @@ void free_runtime(nflow_runtime* rt) {
     if (sw) (void)hipSetDevice(rt->device);
     for (auto* l : rt->int8_layers) nflow_layer_destroy(l);
     for (auto& kv : rt->tw) (void)hipFree(kv.second);
+    for (auto& kv : rt->zfill) (void)hipFree(kv.second);
     if (rt->dblock) (void)hipFree(rt->dblock);
     if (rt->ws) (void)hipFree(rt->ws);
     if (sw) (void)hipSetDevice(cur);
@@ -251,27 +293,42 @@ int init(nflow_runtime* rt) {
     static const char* kOps[] = {"", "FNO1d", "FNO2d", "FNO3d", "DeepONet", "TokenMixer", "GraphOp",
                                  "TokenMixer2D", "GraphOp2D"};
     rt->op = (op >= 1 && op <= 8) ? kOps[op] : "";
-    if (op != 1)
+    if (op != 1 && op != 2)
         return set_error(NFLOW_UNSUPPORTED_OP,
-                         "runtime: the device runtime serves FNO1d (the op with the quantised "
-                         "local-linear path); this IR holds " + rt->op);
+                         "runtime: the device runtime serves FNO1d and FNO2d (the ops with the "
+                         "local-linear layer path); this IR holds " + rt->op);
+    std::memcpy(rt->cfg, cfg, sizeof(rt->cfg));
+    rt->fno2d = op == 2;
     rt->in_ch = cfg[0];
     rt->out_ch = cfg[1];
     rt->width = cfg[2];
-    rt->modes = cfg[3];
-    rt->n_layers = cfg[4];
-    rt->pad_factor = cfg[5];
+    if (rt->fno2d) {
+        // [in_ch, out_ch, width, modes_h, modes_w, n_layers, pad_factor] (ir_loader.h:150-160).
+        rt->modes_h = cfg[3];
+        rt->modes_w = cfg[4];
+        rt->n_layers = cfg[5];
+        rt->pad_factor = cfg[6];
+        rt->modes = rt->modes_h * rt->modes_w;
+    } else {
+        rt->modes = cfg[3];
+        rt->n_layers = cfg[4];
+        rt->pad_factor = cfg[5];
+    }
     rt->act = act == 1 ? RT_ACT_RELU : RT_ACT_GELU;
     rt->quant_enabled = quant != 0;
-    if (rt->in_ch <= 0 || rt->out_ch <= 0 || rt->width <= 0 || rt->modes < 0 || rt->n_layers < 0)
-        return parse_err("bad FNO1d configuration");
+    if (rt->in_ch <= 0 || rt->out_ch <= 0 || rt->width <= 0 || rt->modes_h < 0 || rt->modes_w < 0 || rt->modes < 0 ||
+        rt->n_layers < 0)
+        return parse_err(std::string("bad ") + rt->op + " configuration");
     const int64_t w = rt->width, m = rt->modes;
     if (int rc = take_weight(rt, "lift.weight", {w, rt->in_ch})) return rc;
     if (int rc = take_weight(rt, "lift.bias", {w})) return rc;
     for (int i = 0; i < rt->n_layers; ++i) {
         const std::string s = "specs." + std::to_string(i), l = "locs." + std::to_string(i);
-        if (int rc = take_weight(rt, s + ".weights_real", {w, w, m})) return rc;
-        if (int rc = take_weight(rt, s + ".weights_imag", {w, w, m})) return rc;
+        // (in, out, modes), or (in, out, modes_h, modes_w) for FNO2d.
+        const std::vector<int64_t> sdims =
+            rt->fno2d ? std::vector<int64_t>{w, w, rt->modes_h, rt->modes_w} : std::vector<int64_t>{w, w, m};
+        if (int rc = take_weight(rt, s + ".weights_real", sdims)) return rc;
+        if (int rc = take_weight(rt, s + ".weights_imag", sdims)) return rc;
         if (int rc = take_weight(rt, l + ".weight", {w, w})) return rc;
         if (int rc = take_weight(rt, l + ".bias", {w})) return rc;
     }
@@ -298,7 +355,44 @@ int init(nflow_runtime* rt) {
     rt->lq.assign(rt->n_layers, LayerQuant{});
     bool any_snap = false;
     std::vector<std::pair<std::vector<float>, std::vector<int32_t>>> pos(rt->n_layers);
-    for (int i = 0; i < rt->n_layers && rt->quant_enabled; ++i) {
+    if (rt->fno2d && rt->quant_enabled) {
+        // FNO2d's apply_fake_quant (fno.cpp:810-843): the FP8 qparam of the
+        // key first (the snap when its scale is positive, else nothing),
+        // then the per-tensor INT8 one; no per-token path.
+        auto fq_of = [&](const std::string& key) {
+            FakeQuant f{};
+            int found = 0;
+            float fs = 0.0f;
+            (void)nflow_ir_fp8_qparam(rt->ir, key.c_str(), &found, &fs);
+            if (found) {
+                if (fs > 0.0f) {
+                    f.on = 3;
+                    f.scale = fs;
+                    any_snap = true;
+                }
+                return f;
+            }
+            float s = 1.0f;
+            int32_t z = 0;
+            (void)nflow_ir_per_tensor_qparam(rt->ir, key.c_str(), &found, &s, &z);
+            if (found) {
+                f.on = 1;
+                f.scale = s;
+                f.zpf = static_cast<float>(z);
+            }
+            return f;
+        };
+        rt->fq_lift = fq_of("lift.output");
+        rt->fq_projq = fq_of("proj_q.output");
+        rt->fq_projout = fq_of("proj_out.output");
+        for (int i = 0; i < rt->n_layers; ++i) {
+            const FakeQuant f = fq_of("locs." + std::to_string(i) + ".output");
+            rt->lq[i].x2_kind = f.on;
+            rt->lq[i].x2_scale = f.scale;
+            rt->lq[i].x2_zp = static_cast<int32_t>(f.zpf);
+        }
+    }
+    for (int i = 0; i < rt->n_layers && rt->quant_enabled && !rt->fno2d; ++i) {
         LayerQuant& q = rt->lq[i];
         const std::string in_key = i == 0 ? "lift.output" : "locs." + std::to_string(i - 1) + ".output";
         int found = 0;
@@ -332,6 +426,8 @@ int init(nflow_runtime* rt) {
     }
     if (any_snap && !snap_thresholds(rt->thr))
         return set_error(NFLOW_INTERNAL, "runtime: the host libm's log2 is not monotone at a snap step");
+    for (FakeQuant* f : {&rt->fq_lift, &rt->fq_projq, &rt->fq_projout})
+        std::memcpy(f->thr, rt->thr, sizeof(f->thr));
 
     // Upload: every weight, then the per-position qparams (scales, then zps).
     size_t total = 0;
@@ -397,7 +493,34 @@ const float* twiddle_table(nflow_runtime* rt, int n) {
     return d;
 }
 
+// The zero-column pattern of a column length, uploaded once (FNO2d).
+const float2* zfill_table(nflow_runtime* rt, int n) {
+    auto it = rt->zfill.find(n);
+    if (it != rt->zfill.end()) return reinterpret_cast<const float2*>(it->second);
+    std::vector<float> inv, z;
+    twiddles(n, true, inv);
+    zero_column_ifft(n, inv, z);
+    float* d = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d), z.size() * 4) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, z.data(), z.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    rt->zfill[n] = d;
+    return reinterpret_cast<const float2*>(d);
+}
+
 int check_shapes(const nflow_runtime* rt, const int64_t* xs, int xn, const int64_t* ys, int yn) {
+    if (rt->fno2d) {
+        // FNO2d::Forward's checks, in its order and with its messages (fno.cpp:778-795).
+        if (!xs || xn != 4) return set_error(NFLOW_SHAPE_MISMATCH, "expected 4D input (batch, h, w, in_ch)");
+        if (xs[3] != rt->in_ch) return set_error(NFLOW_SHAPE_MISMATCH, "input channels mismatch");
+        if (!ys || yn != 4 || ys[0] != xs[0] || ys[1] != xs[1] || ys[2] != xs[2] || ys[3] != rt->out_ch)
+            return set_error(NFLOW_SHAPE_MISMATCH, "output buffer shape mismatch");
+        if (!is_pow2(xs[1]) || !is_pow2(xs[2]))
+            return set_error(NFLOW_INVALID_ARG, "FNO2d: H and W must each be a power of two");
+        return NFLOW_OK;
+    }
     // FNO1d::Forward's checks, in its order and with its messages (fno.cpp:409-425).
     if (!xs || xn != 3) return set_error(NFLOW_SHAPE_MISMATCH, "expected 3D input (batch, n, in_ch)");
     if (xs[2] != rt->in_ch) return set_error(NFLOW_SHAPE_MISMATCH, "input channels mismatch");
@@ -509,6 +632,152 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
     return launch_check(launch_linear_ref(po, st), "proj_out");
 }
 
+// FNO2d::Forward on device buffers (fno.cpp:777-995).
+int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, hipStream_t st) {
+    const int64_t b = xs[0];
+    const int H = static_cast<int>(xs[1]), W = static_cast<int>(xs[2]);
+    const int w = rt->width, mh = rt->modes_h, mw = rt->modes_w;
+    int Hp = H, Wp = W;
+    if (rt->pad_factor > 1) {
+        const int pf = rt->pad_factor;
+        Hp = H + (pf - H % pf) % pf;
+        Wp = W + (pf - W % pf) % pf;
+    }
+    const bool padded = Hp != H || Wp != W;
+    if (!is_pow2(Hp) || !is_pow2(Wp))
+        return set_error(NFLOW_INVALID_ARG, "runtime: the padded grid is not a power of two (the FFT needs one)");
+    if (Hp > kFftMaxPoints || Wp > kFftMaxPoints)
+        return set_error(NFLOW_UNSUPPORTED_OP, "runtime: grid sides longer than 8192 points are not supported");
+    if (mh > Hp || mw > Wp / 2 + 1)
+        return set_error(NFLOW_INVALID_ARG, "runtime: modes exceed the bins of the grid");
+    if (b == 0) return NFLOW_OK;
+    const int64_t pts = static_cast<int64_t>(Hp) * Wp, pts0 = static_cast<int64_t>(H) * W;
+    if (pts > INT32_MAX) return set_error(NFLOW_INVALID_ARG, "runtime: the grid exceeds the Linear's int");
+    const float* twW = twiddle_table(rt, Wp);
+    const float* twH = twiddle_table(rt, Hp);
+    const float2* zf = zfill_table(rt, Hp);
+    if (!twW || !twH || !zf) return set_error(NFLOW_INTERNAL, "runtime: twiddle upload failed");
+    const float* twW_inv = twW + 2 * (Wp > 1 ? Wp - 1 : 1);
+    const float* twH_inv = twH + 2 * (Hp > 1 ? Hp - 1 : 1);
+    // Workspace: h (token-major), hc (channel-major), x1c, x2 (b Hp Wp w each),
+    // the row spectra (b w Hp mw complex; reused for the inverse), the kept
+    // corner and its mix (b w mh mw complex each), and with padding the
+    // unpadded grid (b H W w).
+    auto r64 = [](size_t v) { return (v + 63) & ~size_t(63); };
+    const size_t act_e = r64(static_cast<size_t>(b) * pts * w);
+    const size_t row_e = r64(static_cast<size_t>(b) * w * Hp * (mw > 0 ? mw : 1) * 2);
+    const size_t cor_e = r64(static_cast<size_t>(b) * w * (mh * mw > 0 ? mh * mw : 1) * 2);
+    const size_t pad_e = padded ? r64(static_cast<size_t>(b) * pts0 * w) : 0;
+    if (int rc = ensure_ws(rt, (4 * act_e + row_e + 2 * cor_e + pad_e) * sizeof(float))) return rc;
+    float* Hb = static_cast<float*>(rt->ws);
+    float* HC = Hb + act_e;
+    float* X1C = HC + act_e;
+    float* X2 = X1C + act_e;
+    float* R = X2 + act_e;
+    float* S = R + row_e;
+    float* SM = S + cor_e;
+    float* P = SM + cor_e;
+    int log2W = 0, log2H = 0;
+    while ((1 << log2W) < Wp) ++log2W;
+    while ((1 << log2H) < Hp) ++log2H;
+
+    // Lift (fno.cpp:848-852), padding (fno.cpp:867-891), layout change with
+    // lift.output's fake-quant (fno.cpp:852-865; the pads are zeros, which
+    // every fake-quant keeps at +0).
+    const int ip0 = static_cast<int>(pts0);
+    LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), padded ? P : Hb, b, ip0, ip0, ip0, rt->in_ch, w,
+                 RT_ACT_NONE};
+    if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
+    if (padded)
+        if (int rc = launch_check(launch_pad2d(P, Hb, b, H, W, Hp, Wp, w, false, st), "padding")) return rc;
+    if (rt->n_layers > 0) {
+        if (int rc = launch_check(launch_to_channel_major(Hb, HC, b, static_cast<int>(pts), w, rt->fq_lift, st),
+                                  "layout change"))
+            return rc;
+    } else if (int rc = launch_check(launch_fq_act(Hb, b * pts * w, rt->fq_lift, RT_ACT_NONE, st), "lift fake-quant")) {
+        return rc;
+    }
+    for (int i = 0; i < rt->n_layers; ++i) {
+        const LayerQuant& q = rt->lq[i];
+        const std::string si = std::to_string(i);
+        // Spectral convolution (fno.cpp:717-771): rows, kept columns, mix, back.
+        SpecArgs rows{};
+        rows.hc = HC;
+        rows.spec = R;
+        rows.samples = b;
+        rows.w = w * Hp;
+        rows.n = Wp;
+        rows.log2n = log2W;
+        rows.modes = mw;
+        rows.tw_fwd = twW;
+        if (int rc = launch_check(launch_rfft_rows(rows, st), "row FFT")) return rc;
+        ColArgs cf{R, S, twH, b * w, Hp, log2H, mw, mh, 1.0f};
+        if (int rc = launch_check(launch_cfft_cols(cf, false, st), "column FFT")) return rc;
+        SpecArgs mix{};
+        mix.spec = S;
+        mix.spec_mixed = SM;
+        mix.mix_real = rt->dw("mix." + si + ".real");
+        mix.mix_imag = rt->dw("mix." + si + ".imag");
+        mix.samples = b;
+        mix.w = w;
+        mix.modes = mh * mw;
+        if (int rc = launch_check(launch_spec_mix(mix, st), "channel mix")) return rc;
+        ColArgs ci{SM, R, twH_inv, b * w, Hp, log2H, mw, mh, 1.0f / static_cast<float>(Hp)};
+        if (int rc = launch_check(launch_cfft_cols(ci, true, st), "inverse column FFT")) return rc;
+        SpecArgs irows{};
+        irows.spec_mixed = R;
+        irows.x1c = X1C;
+        irows.samples = b;
+        irows.w = w * Hp;
+        irows.n = Wp;
+        irows.log2n = log2W;
+        irows.modes = mw;
+        irows.tw_inv = twW_inv;
+        irows.inv_n = 1.0f / static_cast<float>(Wp);
+        irows.fill = zf;
+        irows.fill_period = Hp;
+        if (int rc = launch_check(launch_irfft_rows(irows, st), "inverse row FFT")) return rc;
+        // Local linear (fno.cpp:906-932), fp32 as in the reference.
+        const int ip = static_cast<int>(pts);
+        LinArgs loc{Hb, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b, ip, ip, ip, w, w,
+                    RT_ACT_NONE};
+        if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        // Tail (fno.cpp:934-945).
+        PostArgs pa{};
+        pa.x2 = X2;
+        pa.x1c = X1C;
+        pa.h = Hb;
+        pa.hc = HC;
+        pa.samples = b;
+        pa.n = ip;
+        pa.w = w;
+        pa.kind = q.x2_kind;
+        pa.scale = q.x2_scale;
+        pa.zpf = static_cast<float>(q.x2_zp);
+        std::memcpy(pa.thr, rt->thr, sizeof(pa.thr));
+        pa.act = rt->act;
+        if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
+    }
+    // Trim (fno.cpp:946-964), proj_q + fake-quant + act, proj_out + fake-quant (fno.cpp:966-993).
+    const float* hsrc = Hb;
+    if (padded) {
+        if (int rc = launch_check(launch_pad2d(Hb, P, b, H, W, Hp, Wp, w, true, st), "trim")) return rc;
+        hsrc = P;
+    }
+    const bool pq_fq = rt->fq_projq.on != 0;
+    LinArgs pq{hsrc, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X2, b, ip0, ip0, ip0, w, w,
+               pq_fq ? static_cast<int>(RT_ACT_NONE) : rt->act};
+    if (int rc = launch_check(launch_linear_ref(pq, st), "proj_q")) return rc;
+    if (pq_fq)
+        if (int rc = launch_check(launch_fq_act(X2, b * pts0 * w, rt->fq_projq, rt->act, st), "proj_q fake-quant"))
+            return rc;
+    LinArgs po{X2, rt->dw("proj_out.weight"), rt->dw("proj_out.bias"), y, b, ip0, ip0, ip0, w, rt->out_ch,
+               RT_ACT_NONE};
+    if (int rc = launch_check(launch_linear_ref(po, st), "proj_out")) return rc;
+    return launch_check(launch_fq_act(y, b * pts0 * rt->out_ch, rt->fq_projout, RT_ACT_NONE, st),
+                        "proj_out fake-quant");
+}
+
 struct DeviceGuard {
     int prev = -1;
     explicit DeviceGuard(int dev) {
@@ -568,13 +837,10 @@ int nflow_runtime_destroy(nflow_runtime* rt) {
 
 const char* nflow_runtime_op(const nflow_runtime* rt) { return rt ? rt->op.c_str() : ""; }
 
-int nflow_runtime_config(const nflow_runtime* rt, int32_t* config6, int* activation, int* quant_enabled) {
+int nflow_runtime_config(const nflow_runtime* rt, int32_t* config7, int* activation, int* quant_enabled) {
     clear_error();
     if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_config: null runtime");
-    if (config6) {
-        const int32_t c[6] = {rt->in_ch, rt->out_ch, rt->width, rt->modes, rt->n_layers, rt->pad_factor};
-        std::memcpy(config6, c, sizeof(c));
-    }
+    if (config7) std::memcpy(config7, rt->cfg, sizeof(rt->cfg));
     if (activation) *activation = rt->act == RT_ACT_RELU ? NFLOW_ACT_RELU : NFLOW_ACT_GELU_TANH;
     if (quant_enabled) *quant_enabled = rt->quant_enabled ? 1 : 0;
     return NFLOW_OK;
@@ -583,6 +849,8 @@ int nflow_runtime_config(const nflow_runtime* rt, int32_t* config6, int* activat
 int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
     clear_error();
     if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm: null runtime");
+    // runtime.cpp:155-166: a no-op for every model but FNO1d.
+    if (rt->fno2d) return NFLOW_OK;
     DeviceGuard g(rt->device);
     for (auto* l : rt->int8_layers) nflow_layer_destroy(l);
     rt->int8_layers.assign(rt->n_layers, nullptr);
@@ -637,6 +905,7 @@ int nflow_runtime_run_device(nflow_runtime* rt, const float* x, const int64_t* x
     if (int rc = check_shapes(rt, x_shape, x_ndim, y_shape, y_ndim)) return rc;
     if (x_shape[0] > 0 && (!x || !y)) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
     DeviceGuard g(rt->device);
+    if (rt->fno2d) return run_device_2d(rt, x, x_shape, y, static_cast<hipStream_t>(stream));
     return run_device(rt, x, x_shape, y, static_cast<hipStream_t>(stream));
 }
 
@@ -645,8 +914,9 @@ int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape,
     clear_error();
     if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_run: null runtime");
     if (int rc = check_shapes(rt, x_shape, x_ndim, y_shape, y_ndim)) return rc;
-    const size_t nx = static_cast<size_t>(x_shape[0] * x_shape[1] * x_shape[2]);
-    const size_t ny = static_cast<size_t>(y_shape[0] * y_shape[1] * y_shape[2]);
+    size_t nx = 1, ny = 1;
+    for (int d = 0; d < x_ndim; ++d) nx *= static_cast<size_t>(x_shape[d]);
+    for (int d = 0; d < y_ndim; ++d) ny *= static_cast<size_t>(y_shape[d]);
     if (nx == 0) return NFLOW_OK;
     if (!x || !y) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
     DeviceGuard g(rt->device);
@@ -659,7 +929,7 @@ int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape,
     }
     int rc = NFLOW_OK;
     if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
-    if (!rc) rc = run_device(rt, dx, x_shape, dy, nullptr);
+    if (!rc) rc = rt->fno2d ? run_device_2d(rt, dx, x_shape, dy, nullptr) : run_device(rt, dx, x_shape, dy, nullptr);
     if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess)
         rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
     if (!rc && hipDeviceSynchronize() != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: device error");

@@ -40,7 +40,7 @@ def test_create_bad_magic(tmp_path):
     assert _lib.lib().nflow_runtime_create(str(p).encode(), C.byref(h)) == _lib.PARSE_ERROR
 
 
-@pytest.mark.parametrize("op", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("op", [3, 4, 5, 6, 7, 8])
 def test_other_ops_are_unsupported(ncpp, tmp_path, op):
     p = tmp_path / "m.nneuroir"
     p.write_bytes(F.header(op, [1, 1, 4, 2, 2, 1, 1]))
@@ -69,6 +69,23 @@ def test_wrong_weight_shape_is_a_parse_error(tmp_path):
     p.write_bytes(F.fno1d_file(w, [2, 1, 8, 4, 1, 1, 0]))
     h = C.c_void_p()
     assert _lib.lib().nflow_runtime_create(str(p).encode(), C.byref(h)) == _lib.PARSE_ERROR
+
+
+def test_fno2d_weights_are_checked(tmp_path):
+    # FNO2d is served: its weights are read in LoadBinary's order with the
+    # (in, out, modes_h, modes_w) spectral shape (ir_loader.h:298-322).
+    rng = np.random.default_rng(5)
+    cfg = [2, 1, 8, 3, 4, 2, 1]
+    p = tmp_path / "m.nneuroir"
+    p.write_bytes(F.header(2, cfg))
+    h = C.c_void_p()
+    assert _lib.lib().nflow_runtime_create(str(p).encode(), C.byref(h)) == _lib.PARSE_ERROR
+    assert b"lift.weight" in _lib.lib().nflow_last_error()
+    w = F.fno2d_weights(rng, 2, 1, 8, 3, 4, 2)
+    w["specs.1.weights_imag"] = w["specs.1.weights_imag"][:, :, :, :3]
+    p.write_bytes(F.fno2d_file(w, cfg))
+    assert _lib.lib().nflow_runtime_create(str(p).encode(), C.byref(h)) == _lib.PARSE_ERROR
+    assert b"specs.1.weights_imag" in _lib.lib().nflow_last_error()
 
 
 def test_deeponet_arrays_messages(ncpp, tmp_path):
