@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d"])
+                    choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d", "fno2d"])
     ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--check", action="store_true", default=True)
@@ -173,10 +173,11 @@ def cpu_baseline(wl, layers, args):
     }
 
 
-def ref_runtime_baseline(model, threads_all):
-    """The reference runtime itself (InferenceRuntime over FNO1d with
-    EnableInt8Gemm, oracle/_ref/ref_fno_run built from its sources) on the
-    host cores over a bounded sample of the same batch."""
+def ref_runtime_baseline(model, threads_all, b_all=16, b_one=16, reps=3):
+    """The reference runtime itself (InferenceRuntime with EnableInt8Gemm,
+    oracle/_ref/ref_fno_run built from its sources) on the host cores over a
+    bounded sample of the same batch: b_all samples over all threads, b_one
+    on one thread."""
     import subprocess
     import tempfile
 
@@ -186,25 +187,23 @@ def ref_runtime_baseline(model, threads_all):
     exe = ROOT / "oracle" / "_ref" / "ref_fno_run"
     if not exe.exists():
         raise FileNotFoundError(f"{exe} not built")
-    b_s = 16
-    x = np.ascontiguousarray(model.x[:b_s])
-    _, n, ci = x.shape
-    co = model.config[1]
+    grid = "x".join(str(d) for d in model.x.shape[1:-1])
+    ci, co = model.x.shape[-1], model.config[1]
     with tempfile.TemporaryDirectory() as d:
-        ir, xf, yf = Path(d) / "m.nneuroir", Path(d) / "x.f32", Path(d) / "y.f32"
+        ir, xf = Path(d) / "m.nneuroir", Path(d) / "x.f32"
         ir.write_bytes(model.ir)
-        x.tofile(xf)
+        np.ascontiguousarray(model.x[:max(b_all, b_one)]).tofile(xf)
         rates = {}
-        for threads in (1, threads_all):
-            out = subprocess.run([str(exe), str(ir), str(xf), str(b_s), str(n), str(ci), str(co), str(yf), "int8",
-                                  "3", str(threads)], capture_output=True, text=True, check=True).stdout
+        for threads, b_s in ((1, b_one), (threads_all, b_all)):
+            out = subprocess.run([str(exe), str(ir), str(xf), str(b_s), grid, str(ci), str(co), "-", "int8",
+                                  str(reps), str(threads)], capture_output=True, text=True, check=True).stdout
             us = float(out.split("us_per_run")[1].split()[0])
             rates[threads] = b_s / (us * 1e-6)
     return {"value": rates[threads_all], "unit": "samples/s", "cores": threads_all, "kind": "reference",
             "sample": (f"InferenceRuntime::Run with EnableInt8Gemm (the reference runtime built from its "
-                       f"sources: runtime.cpp, fno.cpp, fft.cpp, int8_gemm.cpp VNNI) on {b_s} of the "
-                       f"batch's samples, median of 3 runs, samples split over {threads_all} threads with "
-                       f"one runtime each, and on 1 thread; host {O.host_cpu_model()}"),
+                       f"sources: runtime.cpp, fno.cpp, fft.cpp, int8_gemm.cpp VNNI) on {b_all} of the "
+                       f"batch's samples split over {threads_all} threads with one runtime each, and on "
+                       f"{b_one} samples on 1 thread, median of {reps} runs; host {O.host_cpu_model()}"),
             "value_1core": rates[1]}
 
 
@@ -213,33 +212,59 @@ def bench_fno1d_model(args):
     InferenceRuntime run (lift, 4 x [input fake-quant, spectral convolution,
     INT8 local-linear layer, act(x1 + x2)], proj_q, proj_out) over the batch,
     with its input already in HBM."""
+    from neuroflow_amd import workloads as WL
+    from oracle import fno1d as OF
+
+    def oracle_forward(model, x):
+        m = OF.from_records(model.config, False, model.weights, model.qparams)
+        OF.enable_int8_gemm(m)
+        return OF.forward(m, x)
+
+    bench_runtime_model(args, WL.fno1d_model(), oracle_forward, "int8", 16, 16)
+
+
+def bench_fno2d_model(args):
+    """The whole FNO2d model through the device runtime: one step = one
+    InferenceRuntime run (lift, 4 x [row / column FFTs, 12 x 12 mode mix,
+    inverse FFTs, local linear, FP8 snap of x2, act(x1 + x2)], proj_q,
+    proj_out) over the batch, with its input already in HBM."""
+    from neuroflow_amd import workloads as WL
+    from oracle import fno2d as OF2
+
+    def oracle_forward(model, x):
+        return OF2.forward(OF2.from_records(model.config, False, model.weights, model.qparams), x)
+
+    bench_runtime_model(args, WL.fno2d_model(), oracle_forward, "fp32", 16, 1, 1)
+
+
+def bench_runtime_model(args, model, oracle_forward, dtype, cpu_b_all, cpu_b_one, cpu_reps=3):
     import ctypes as C
 
     import numpy as np
     import torch
     from neuroflow_amd import _lib
-    from neuroflow_amd import workloads as WL
 
     L = _lib.lib()
     dev = torch.device("cuda:0")
-    model = WL.fno1d_model()
     h = C.c_void_p()
     buf = C.create_string_buffer(model.ir, len(model.ir))
     _lib.check(L.nflow_runtime_create_memory(buf, len(model.ir), C.byref(h)), "runtime_create")
     _lib.check(L.nflow_runtime_enable_int8_gemm(h), "runtime_enable_int8_gemm")
-    b, n, ci = model.x.shape
+    b = model.x.shape[0]
     co = model.config[1]
-    xsh = (C.c_int64 * 3)(b, n, ci)
-    ysh = (C.c_int64 * 3)(b, n, co)
+    ys_shape = list(model.x.shape[:-1]) + [co]
+    nd = model.x.ndim
+    xsh = (C.c_int64 * nd)(*model.x.shape)
+    ysh = (C.c_int64 * nd)(*ys_shape)
     n_sets = 4
     xs = [torch.from_numpy(model.x).to(dev) for _ in range(n_sets)]
-    ys = [torch.empty(b, n, co, dtype=torch.float32, device=dev) for _ in range(n_sets)]
+    ys = [torch.empty(*ys_shape, dtype=torch.float32, device=dev) for _ in range(n_sets)]
     stream = torch.cuda.current_stream()
     sptr = stream.cuda_stream
     fn = L.nflow_runtime_run_device
 
     def step(i):
-        _lib.check(fn(h, xs[i % n_sets].data_ptr(), xsh, 3, ys[i % n_sets].data_ptr(), ysh, 3, sptr),
+        _lib.check(fn(h, xs[i % n_sets].data_ptr(), xsh, nd, ys[i % n_sets].data_ptr(), ysh, nd, sptr),
                    "runtime_run_device")
 
     for i in range(max(1, args.warmup)):
@@ -255,13 +280,11 @@ def bench_fno1d_model(args):
 
     parity = None
     if args.check:
-        from oracle import fno1d as OF
-        m = OF.from_records(model.config, False, model.weights, model.qparams)
-        OF.enable_int8_gemm(m)
-        want = OF.forward(m, model.x[:2])
-        y2 = torch.empty(2, n, co, dtype=torch.float32, device=dev)
-        _lib.check(fn(h, xs[0].data_ptr(), (C.c_int64 * 3)(2, n, ci), 3, y2.data_ptr(),
-                      (C.c_int64 * 3)(2, n, co), 3, sptr), "runtime_run_device")
+        b2 = 2 if nd == 3 else 1
+        want = oracle_forward(model, model.x[:b2])
+        y2 = torch.empty(b2, *ys_shape[1:], dtype=torch.float32, device=dev)
+        _lib.check(fn(h, xs[0].data_ptr(), (C.c_int64 * nd)(b2, *model.x.shape[1:]), nd, y2.data_ptr(),
+                      (C.c_int64 * nd)(b2, *ys_shape[1:]), nd, sptr), "runtime_run_device")
         torch.cuda.synchronize()
         parity = bool(np.array_equal(y2.cpu().numpy().view(np.uint32), want.view(np.uint32)))
 
@@ -269,7 +292,7 @@ def bench_fno1d_model(args):
     if not args.no_cpu_baseline:
         try:
             from oracle import oracle as O
-            cpu = ref_runtime_baseline(model, O.usable_cores())
+            cpu = ref_runtime_baseline(model, O.usable_cores(), cpu_b_all, cpu_b_one, cpu_reps)
         except Exception as e:  # reported, not fatal
             cpu = {"error": f"{type(e).__name__}: {e}"}
     L.nflow_runtime_destroy(h)
@@ -284,9 +307,9 @@ def bench_fno1d_model(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": dtype,
         "data": "synthetic (seeded SplitMix64 input fields, seeded PyTorch-style initial weights)",
-        "config": {"workload": model.name, "batch": b, "points": n, "config": model.config,
+        "config": {"workload": model.name, "batch": b, "grid": list(model.x.shape[1:-1]), "config": model.config,
                    "parallelism": "single GPU"},
         "roofline": None,
         "cpu_baseline": cpu,
@@ -304,6 +327,9 @@ def main():
         sys.exit(2)
     if args.workload == "fno1d":
         bench_fno1d_model(args)
+        return
+    if args.workload == "fno2d":
+        bench_fno2d_model(args)
         return
 
     import numpy as np

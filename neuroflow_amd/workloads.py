@@ -258,6 +258,76 @@ def fno1d_model(batch: int = 256, n_points: int = 1024, width: int = 64, modes: 
                       f"modes {modes}, {n_layers} layers, INT8 local-linear layers, GELU)", ir, x, cfg, weights, q)
 
 
+def sinusoid_fields_2d(sid: int, batch: int, h: int, w: int, n_terms: int) -> np.ndarray:
+    """u_b(x, y) = sum_j A_j sin(2 pi (kx_j x + ky_j y) + phi_j) on the
+    (h, w) grid x = i / h, y = j / w; A ~ U(0,1), kx, ky uniform on 1..16,
+    phi ~ U(0, 2 pi).  Returns (batch, h, w)."""
+    amp = uniform(sid, (batch, n_terms)).astype(np.float64)
+    kx = np.floor(uniform(sid + 1, (batch, n_terms)).astype(np.float64) * 16.0) + 1.0
+    ky = np.floor(uniform(sid + 2, (batch, n_terms)).astype(np.float64) * 16.0) + 1.0
+    phi = uniform(sid + 3, (batch, n_terms)).astype(np.float64) * 2.0 * math.pi
+    xs = (np.arange(h, dtype=np.float64) / h)[:, None]
+    ys = (np.arange(w, dtype=np.float64) / w)[None, :]
+    out = np.zeros((batch, h, w), np.float64)
+    for j in range(n_terms):
+        arg = 2.0 * math.pi * (kx[:, j, None, None] * xs + ky[:, j, None, None] * ys) + phi[:, j, None, None]
+        out += amp[:, j, None, None] * np.sin(arg)
+    return out.astype(np.float32)
+
+
+def fno2d_model(batch: int = 16, grid: int = 256, width: int = 64, modes: int = 12,
+                n_layers: int = 4) -> Fno1dModel:
+    """C3's FNO2d as a whole model (batch 16 x 256 x 256 grid, width 64,
+    modes 12 x 12, 4 layers, GELU) with the runtime's FP8 semantics: the
+    NIRQ block carries FP8 E4M3 activation qparams (scale absmax / 448 over
+    the first sample, from a float64 pass of the same forward) for
+    lift.output, every locs.{i}.output and proj_q.output, which FNO2d::Forward
+    applies as its log2 snap (fno.cpp:810-829).  Weights seeded as the
+    reference's PyTorch modules initialise them."""
+    from .ir import write_binary
+
+    w, m = width, modes
+    rng_id = 700
+    weights = {"lift.weight": uniform(rng_id, (w, 1), -1.0, 1.0), "lift.bias": uniform(rng_id + 1, (w,), -1.0, 1.0)}
+    for i in range(n_layers):
+        sc = 1.0 / (w * w)
+        weights[f"specs.{i}.weights_real"] = (sc * normal(rng_id + 10 + 4 * i, (w, w, m, m))).astype(np.float32)
+        weights[f"specs.{i}.weights_imag"] = (sc * normal(rng_id + 11 + 4 * i, (w, w, m, m))).astype(np.float32)
+        weights[f"locs.{i}.weight"] = kaiming_uniform(rng_id + 12 + 4 * i, w, w)
+        b = 1.0 / math.sqrt(w)
+        weights[f"locs.{i}.bias"] = uniform(rng_id + 13 + 4 * i, (w,), -b, b)
+    b = 1.0 / math.sqrt(w)
+    weights["proj_q.weight"] = kaiming_uniform(rng_id + 90, w, w)
+    weights["proj_q.bias"] = uniform(rng_id + 91, (w,), -b, b)
+    weights["proj_out.weight"] = kaiming_uniform(rng_id + 92, 1, w)
+    weights["proj_out.bias"] = uniform(rng_id + 93, (1,), -b, b)
+    x = sinusoid_fields_2d(210, batch, grid, grid, 8)[..., None].astype(np.float32)
+
+    # Calibration pass (float64, one sample, channel-last): absmax of each activation.
+    def gelu(z):
+        return 0.5 * z * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (z + 0.044715 * z ** 3)))
+
+    h = x[:1].astype(np.float64) @ weights["lift.weight"].T.astype(np.float64) + weights["lift.bias"]
+    amax = {"lift.output": float(np.abs(h).max())}
+    for i in range(n_layers):
+        spec = np.fft.rfft2(h, axes=(1, 2))[:, :m, :m, :]                 # (b, m, m, w_in)
+        wc = weights[f"specs.{i}.weights_real"] + 1j * weights[f"specs.{i}.weights_imag"]
+        mixed = np.einsum("bxyi,ioxy->bxyo", spec, wc)
+        full = np.zeros((h.shape[0], grid, grid // 2 + 1, w), np.complex128)
+        full[:, :m, :m, :] = mixed
+        x1 = np.fft.irfft2(full, s=(grid, grid), axes=(1, 2))
+        x2 = h @ weights[f"locs.{i}.weight"].T.astype(np.float64) + weights[f"locs.{i}.bias"]
+        amax[f"locs.{i}.output"] = float(np.abs(x2).max())
+        h = gelu(x1 + x2)
+    amax["proj_q.output"] = float(np.abs(h @ weights["proj_q.weight"].T.astype(np.float64)
+                                         + weights["proj_q.bias"]).max())
+    q = [(3, key, float(np.float32(a) / np.float32(448.0))) for key, a in amax.items()]
+    cfg = [1, 1, w, m, m, n_layers, 1]
+    ir = write_binary(2, cfg, "gelu", weights, q)
+    return Fno1dModel(f"FNO2d model, C3 configuration (batch {batch} x {grid}x{grid} grid, width {w}, "
+                      f"modes {m}x{m}, {n_layers} layers, FP8 activation snap, GELU)", ir, x, cfg, weights, q)
+
+
 WORKLOADS = {
     "c1": c1_standalone,
     "c2": c2_fno1d,

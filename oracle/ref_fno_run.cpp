@@ -9,7 +9,8 @@
 //
 // <n> is the grid: "n" for a 1-D model (shapes (batch, n, ch)) or "HxW" for
 // FNO2d (shapes (batch, H, W, ch)).
-// "int8" calls EnableInt8Gemm() before Run.  Prints "status <code>".  With
+// "int8" calls EnableInt8Gemm() before Run.  Prints "status <code>".  A
+// <y.f32> of "-" skips the first (untimed, output-writing) run.  With
 // reps > 0 it then times `reps` runs of the whole batch, split by samples
 // over `threads` std::threads that each hold their own InferenceRuntime
 // (FNO1d::Forward is single-threaded; one runtime per thread keeps its
@@ -54,12 +55,15 @@ int main(int argc, char** argv) {
     std::unique_ptr<nflow::InferenceRuntime> rt;
     nflow::Status s = nflow::InferenceRuntime::Create(argv[1], rt);
     if (s.ok() && int8) rt->EnableInt8Gemm();
-    if (s.ok()) s = rt->Run(x.data(), shape(b, ci), y.data(), shape(b, co));
+    const bool write_y = std::string(argv[7]) != "-";
+    if (s.ok() && write_y) s = rt->Run(x.data(), shape(b, ci), y.data(), shape(b, co));
     std::printf("status %d\n", static_cast<int>(s.code()));
     if (!s.ok()) return 0;
-    FILE* fy = std::fopen(argv[7], "wb");
-    if (!fy || std::fwrite(y.data(), sizeof(float), y.size(), fy) != y.size()) return 4;
-    std::fclose(fy);
+    if (write_y) {
+        FILE* fy = std::fopen(argv[7], "wb");
+        if (!fy || std::fwrite(y.data(), sizeof(float), y.size(), fy) != y.size()) return 4;
+        std::fclose(fy);
+    }
     if (reps <= 0) return 0;
 
     const int T = static_cast<int>(std::min<int64_t>(threads, b));
