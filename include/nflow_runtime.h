@@ -56,6 +56,15 @@ int nflow_runtime_config(const nflow_runtime* rt, int32_t* config7, int* activat
  * LinearForwardBatched when LinearDispatchTryInt8 would take it
  * (fno.cpp:125-159).  A no-op for FNO2d, as in the reference. */
 int nflow_runtime_enable_int8_gemm(nflow_runtime* rt);
+/* No counterpart in the reference, whose FNO2d has no EnableInt8Gemm: for
+ * FNO2d models, the same cache and dispatch as EnableInt8Gemm does for FNO1d
+ * (fno.cpp:125-159, 360-406).  Each locs.{i} whose weight has axis-0
+ * per-channel qparams, and whose input key (lift.output / locs.{i-1}.output)
+ * has a per-tensor qparam and no FP8 or per-token one, then runs as the INT8
+ * LinearForwardBatched + bias instead of the fp32 Linear.  For callers that
+ * want C3's model on the INT8 GEMM; nflow_runtime_enable_int8_gemm stays the
+ * reference's no-op for FNO2d.  UnsupportedOp for other models. */
+int nflow_runtime_enable_int8_gemm_fno2d(nflow_runtime* rt);
 /* InferenceRuntime::IsInt8GemmEnabled (runtime.h:103, runtime.cpp:168-171). */
 int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled);
 /* Whether locs.{layer_index} runs on the INT8 GEMM. */
@@ -140,6 +149,8 @@ public:
     }
     const std::string& op() const { return op_; }
     void EnableInt8Gemm() { (void)nflow_runtime_enable_int8_gemm(h_); }
+    // No reference counterpart: the FNO2d INT8 opt-in above.
+    Status EnableInt8GemmFno2d() { return status_from(nflow_runtime_enable_int8_gemm_fno2d(h_)); }
     bool IsInt8GemmEnabled() const {
         int e = 0;
         return nflow_runtime_is_int8_gemm_enabled(h_, &e) == NFLOW_OK && e != 0;

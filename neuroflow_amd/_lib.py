@@ -136,6 +136,7 @@ SIGNATURES = {
     "nflow_runtime_op": [_vp],
     "nflow_runtime_config": [_vp, C.POINTER(C.c_int32), C.POINTER(_i32), C.POINTER(_i32)],
     "nflow_runtime_enable_int8_gemm": [_vp],
+    "nflow_runtime_enable_int8_gemm_fno2d": [_vp],
     "nflow_runtime_is_int8_gemm_enabled": [_vp, C.POINTER(_i32)],
     "nflow_runtime_layer_dispatch": [_vp, _i32, C.POINTER(_i32)],
     "nflow_runtime_run": [_vp, _vp, C.POINTER(C.c_int64), _i32, _vp, C.POINTER(C.c_int64), _i32],

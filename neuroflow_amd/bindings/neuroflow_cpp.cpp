@@ -9,7 +9,9 @@
 //   infer_deeponet_arrays(model_path, u, y)        (DeepONet: not served)
 //   InferenceRuntime(path): op(), enable_int8_gemm(), is_int8_gemm_enabled(),
 //                           run(x, y), and run_device(x_ptr, x_shape,
-//                           y_ptr, y_shape, stream=0) on device pointers
+//                           y_ptr, y_shape, stream=0) on device pointers;
+//                           enable_int8_gemm_fno2d() (FNO2d only, no reference
+//                           counterpart)
 //   fp8_e4m3_fake_quant(in, scale), fp8_e4m3_to_bits(in), fp8_e4m3_from_bits(in)
 //
 // The runtime serves FNO1d and FNO2d (include/nflow_runtime.h); creating it
@@ -160,6 +162,14 @@ PYBIND11_MODULE(neuroflow_cpp, m) {
         .def("enable_int8_gemm", &nflow::InferenceRuntime::EnableInt8Gemm,
              "Route FNO1d's per-layer local Linear through the INT8 GEMM on the GPU. "
              "No-op for non-FNO1d models.")
+        .def(
+            "enable_int8_gemm_fno2d",
+            [](nflow::InferenceRuntime& self) {
+                const nflow::Status s = self.EnableInt8GemmFno2d();
+                if (!s.ok()) throw std::runtime_error("enable_int8_gemm_fno2d failed: " + s.message());
+            },
+            "FNO2d only (no counterpart in the reference): run the local linear layers on the INT8 GEMM "
+            "with FNO1d's dispatch conditions.")
         .def("is_int8_gemm_enabled", &nflow::InferenceRuntime::IsInt8GemmEnabled,
              "True iff enable_int8_gemm was effective.")
         .def(

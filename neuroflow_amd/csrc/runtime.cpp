@@ -737,11 +737,20 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
         irows.fill = zf;
         irows.fill_period = Hp;
         if (int rc = launch_check(launch_irfft_rows(irows, st), "inverse row FFT")) return rc;
-        // Local linear (fno.cpp:906-932), fp32 as in the reference.
+        // Local linear (fno.cpp:906-932): fp32 as in the reference, or, after
+        // the FNO2d INT8 opt-in, FNO1d's INT8 branch (LinearForwardBatched
+        // with the input key's per-tensor qparam, then + bias).
         const int ip = static_cast<int>(pts);
-        LinArgs loc{Hb, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b, ip, ip, ip, w, w,
-                    RT_ACT_NONE};
-        if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        if (q.int8 && rt->int8_enabled) {
+            if (b * pts > INT32_MAX)
+                return set_error(NFLOW_INVALID_ARG, "runtime: batch * points exceeds the batched API's int");
+            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], b * pts, Hb, X2, q.sa, q.zpa, st))
+                return rc;
+        } else {
+            LinArgs loc{Hb, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b, ip, ip, ip, w,
+                        w, RT_ACT_NONE};
+            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        }
         // Tail (fno.cpp:934-945).
         PostArgs pa{};
         pa.x2 = X2;
@@ -846,11 +855,13 @@ int nflow_runtime_config(const nflow_runtime* rt, int32_t* config7, int* activat
     return NFLOW_OK;
 }
 
-int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
-    clear_error();
-    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm: null runtime");
-    // runtime.cpp:155-166: a no-op for every model but FNO1d.
-    if (rt->fno2d) return NFLOW_OK;
+}  // extern "C"
+
+namespace nfq {
+namespace {
+// EnableInt8Gemm's cache of the dispatched layers (fno.cpp:360-406) and the
+// per-layer decision of LinearDispatchTryInt8 (fno.cpp:125-159).
+int build_int8_layers(nflow_runtime* rt) {
     DeviceGuard g(rt->device);
     for (auto* l : rt->int8_layers) nflow_layer_destroy(l);
     rt->int8_layers.assign(rt->n_layers, nullptr);
@@ -880,6 +891,27 @@ int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
         q.int8 = use != 0;
     }
     return NFLOW_OK;
+}
+}  // namespace
+}  // namespace nfq
+
+extern "C" {
+
+int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm: null runtime");
+    // runtime.cpp:155-166: a no-op for every model but FNO1d.
+    if (rt->fno2d) return NFLOW_OK;
+    return build_int8_layers(rt);
+}
+
+int nflow_runtime_enable_int8_gemm_fno2d(nflow_runtime* rt) {
+    clear_error();
+    if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm_fno2d: null runtime");
+    if (!rt->fno2d)
+        return set_error(NFLOW_UNSUPPORTED_OP, "runtime_enable_int8_gemm_fno2d: the model is " + rt->op +
+                                                   " (FNO1d has EnableInt8Gemm)");
+    return build_int8_layers(rt);
 }
 
 int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled) {

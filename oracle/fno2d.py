@@ -34,7 +34,10 @@ class Fno2dModel:
     act_tensor: Dict[str, Tuple[float, int]] = field(default_factory=dict)
     weight_tensor: Dict[str, Tuple[float, int]] = field(default_factory=dict)
     per_channel: Dict[str, Tuple[np.ndarray, np.ndarray, int]] = field(default_factory=dict)
+    per_token: Dict[str, Tuple[np.ndarray, np.ndarray, int]] = field(default_factory=dict)
     fp8: Dict[str, float] = field(default_factory=dict)
+    int8_cache: Dict[str, Tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]] = field(default_factory=dict)
+    int8_enabled: bool = False
 
 
 def weight_names(n_layers: int) -> List[str]:
@@ -63,6 +66,8 @@ def from_records(cfg, act_relu: bool, weights: Dict[str, np.ndarray],
                 tgt[name] = (np.float32(p[0]), int(p[1]))
             elif kind == 1:
                 m.per_channel[name] = (np.asarray(p[0], np.float32), np.asarray(p[1], np.int32), int(p[2]))
+            elif kind == 2:
+                m.per_token[name] = (np.asarray(p[0], np.float32), np.asarray(p[1], np.int32), int(p[2]))
             elif kind == 3:
                 m.fp8[name] = np.float32(p[0])
         _dequantise_weights(m)
@@ -90,6 +95,25 @@ def _dequantise_weights(m: Fno2dModel):
         pt = m.weight_tensor.get(name)
         if pt is not None:
             m.weights[name] = O.fake_quant_elementwise(t, pt[0], pt[1])
+
+
+def enable_int8_gemm_fno2d(m: Fno2dModel):
+    """The device runtime's FNO2d INT8 opt-in, which has no counterpart in
+    the reference: FNO1d's cache (fno.cpp:360-406, an INT8 blob by
+    QuantiseWeight2D for each locs.{i} weight with 2-D axis-0 per-channel
+    qparams) and its dispatch (LinearDispatchTryInt8, fno.cpp:125-159)."""
+    m.int8_enabled = True
+    m.int8_cache = {}
+    for i in range(m.n_layers):
+        name = f"locs.{i}.weight"
+        pc = m.per_channel.get(name)
+        W = m.weights[name]
+        if pc is None or W.ndim != 2 or pc[2] != 0:
+            continue
+        scales = np.ascontiguousarray(pc[0][:W.shape[0]], np.float32)
+        zps = np.ascontiguousarray(pc[1][:W.shape[0]], np.int32)
+        Wq, sumw = O.quantise_weight_2d(W, scales, zps)
+        m.int8_cache[name] = (Wq, scales, zps, sumw)
 
 
 def fake_quant(m: Fno2dModel, data: np.ndarray, key: str) -> np.ndarray:
@@ -132,7 +156,18 @@ def forward(m: Fno2dModel, x: np.ndarray) -> np.ndarray:
         x1 = O.spectral_conv2d(h_perm, Wt[f"specs.{i}.weights_real"], Wt[f"specs.{i}.weights_imag"],
                                m.modes_h, m.modes_w)
         x2_in = np.ascontiguousarray(h_perm.transpose(0, 2, 3, 1)).reshape(b * H * W, w)
-        x2_out = O.linear_f32(x2_in, Wt[f"locs.{i}.weight"], Wt[f"locs.{i}.bias"])
+        in_key = "lift.output" if i == 0 else f"locs.{i - 1}.output"
+        cache_key = f"locs.{i}.weight"
+        use_int8 = (m.int8_enabled and in_key not in m.per_token and in_key not in m.fp8
+                    and cache_key in m.int8_cache and in_key in m.act_tensor)
+        if use_int8:
+            Wq, sw, zw, sumw = m.int8_cache[cache_key]
+            s_a, zp_a = m.act_tensor[in_key]
+            rc, x2_out = O.linear_forward_batched(x2_in, Wq, sw, zw, None, s_a, zp_a, sumw)
+            assert rc == 0
+            x2_out = (x2_out + Wt[f"locs.{i}.bias"][None, :]).astype(np.float32)
+        else:
+            x2_out = O.linear_f32(x2_in, Wt[f"locs.{i}.weight"], Wt[f"locs.{i}.bias"])
         x2 = np.ascontiguousarray(x2_out.reshape(b, H, W, w).transpose(0, 3, 1, 2))
         x2 = fake_quant(m, x2, f"locs.{i}.output")
         h_perm = O.apply_activation((x1 + x2).astype(np.float32), m.act)

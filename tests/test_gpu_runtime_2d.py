@@ -10,6 +10,7 @@ infer_arrays)."""
 import numpy as np
 import pytest
 
+from neuroflow_amd import _lib
 from neuroflow_amd.runtime import load
 from oracle import fno2d as OF2
 from tests import nir_format as F
@@ -130,3 +131,59 @@ def test_padded_grid_must_be_a_power_of_two(gpu, tmp_path):
     rt = ncpp.InferenceRuntime(str(path))
     with pytest.raises(RuntimeError, match="padded grid is not a power of two"):
         rt.run(x, np.zeros((1, 4, 4, 1), np.float32))
+
+
+INT8_CASES = [
+    # (b, H, W, in, out, width, mh, mw, layers, pad, relu, quant kinds)
+    (2, 16, 16, 2, 1, 16, 4, 4, 3, 1, False, ["tensor"]),
+    (2, 16, 8, 1, 2, 8, 3, 3, 4, 1, True, ["tensor", "fp8"]),      # fp8 inputs keep those layers fp32
+    (1, 4, 4, 1, 1, 4, 2, 2, 2, 8, False, ["tensor"]),             # padded
+    (2, 64, 64, 1, 1, 64, 12, 12, 2, 1, False, ["tensor"]),
+]
+
+
+@pytest.mark.parametrize("case", INT8_CASES, ids=_ids)
+def test_int8_opt_in_bit_exact(gpu, tmp_path, case):
+    """The FNO2d INT8 opt-in (no counterpart in the reference): each
+    dispatched locs.{i} runs as LinearForwardBatched + bias with its input
+    key's per-tensor qparam, bit-exact against the oracle composed of the
+    reference's primitives; the reference's own enable_int8_gemm stays a
+    no-op."""
+    import ctypes as C
+    ncpp = load()
+    ir, x, m = _model(case, seed=13)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    b, H, W, _ = x.shape
+    rt = ncpp.InferenceRuntime(str(path))
+    rt.enable_int8_gemm()
+    y_fp32 = np.zeros((b, H, W, case[4]), np.float32)
+    rt.run(x, y_fp32)
+    assert np.array_equal(_bits(y_fp32), _bits(OF2.forward(m, x)))
+    rt.enable_int8_gemm_fno2d()
+    assert rt.is_int8_gemm_enabled()
+    OF2.enable_int8_gemm_fno2d(m)
+    y = np.zeros_like(y_fp32)
+    rt.run(x, y)
+    want = OF2.forward(m, x)
+    assert np.array_equal(_bits(y), _bits(want)), int((_bits(y) != _bits(want)).sum())
+    # The per-layer decision is the one FNO1d's dispatch would take.
+    h = C.c_void_p()
+    _lib.check(_lib.lib().nflow_runtime_create(str(path).encode(), C.byref(h)), "runtime_create")
+    _lib.check(_lib.lib().nflow_runtime_enable_int8_gemm_fno2d(h), "enable_int8_gemm_fno2d")
+    for i in range(case[8]):
+        used = C.c_int32()
+        _lib.check(_lib.lib().nflow_runtime_layer_dispatch(h, i, C.byref(used)), "layer_dispatch")
+        in_key = "lift.output" if i == 0 else f"locs.{i - 1}.output"
+        assert bool(used.value) == (in_key in m.act_tensor and in_key not in m.fp8)
+    _lib.lib().nflow_runtime_destroy(h)
+
+
+def test_int8_opt_in_rejects_fno1d(gpu, tmp_path):
+    ncpp = load()
+    rng = np.random.default_rng(9)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(F.fno1d_file(F.fno1d_weights(rng, 2, 1, 8, 4, 1), [2, 1, 8, 4, 1, 1, 0]))
+    rt = ncpp.InferenceRuntime(str(path))
+    with pytest.raises(RuntimeError, match="enable_int8_gemm_fno2d failed"):
+        rt.enable_int8_gemm_fno2d()
