@@ -25,17 +25,20 @@ static void launch_gemm_t(const RowsArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, st, a, groups);
 }
 
-// Tile shape: 128 x 256 for large M and N (two blocks per CU), else
-// 128 x 128 (more blocks for the small-M / narrow-N shapes).  Measured on
-// MI355X: 256 x 256 (one wave per SIMD) never beats 128 x 256, and 128 x 128
-// wins for M <= 4096 or N <= 768.
+// Tile shape: 128 x 256 for large M and N (two blocks per CU); 64 x 128 for
+// M <= 4096 with N >= 512 (twice the blocks of 128 x 128: at C5's branch,
+// M = 4096, K = N = 1024, 12.6 us against 13.7 us, and 14.2 us at 64 x 64);
+// else 128 x 128.  Measured on MI355X: 256 x 256 (one wave per SIMD) never
+// beats 128 x 256, 64 x 128 loses at the trunk (173 us against 139 us).
 static int gemm_shape(const RowsArgs& a) {
-    // NFLOW_GEMM_TILE=88|48|44 forces a shape (for tile sweeps).
+    // NFLOW_GEMM_TILE=88|48|44|24|22 forces a shape (for tile sweeps; 22 and 24 only
+    // on the LDS-DMA kernel).
     if (const char* f = std::getenv("NFLOW_GEMM_TILE")) {
         const int t = std::atoi(f);
-        if (t == 88 || t == 48 || t == 44) return t;
+        if (t == 88 || t == 48 || t == 44 || t == 22 || t == 24) return t;
     }
-    return (a.M >= 16384 && a.N >= 1024) ? 48 : 44;
+    if (a.M >= 16384 && a.N >= 1024) return 48;
+    return (a.M <= 4096 && a.N >= 512) ? 24 : 44;
 }
 
 template <int TM, int TN, int OUT, int ACT>
@@ -62,6 +65,8 @@ static void launch_gemm_act(const RowsArgs& a, hipStream_t st) {
     const int shape = gemm_shape(a);
     if (shape != 88 && gemm_pipe_ok(a, OUT)) {
         if (shape == 48) launch_pipe_t<4, 8, OUT, ACT>(a, st);
+        else if (shape == 22) launch_pipe_t<2, 2, OUT, ACT>(a, st);
+        else if (shape == 24) launch_pipe_t<2, 4, OUT, ACT>(a, st);
         else launch_pipe_t<4, 4, OUT, ACT>(a, st);
         return;
     }

@@ -1,5 +1,8 @@
 """GPU parity of the INT8 path against the oracle (bit-exact codes, int32
 accumulators and dequantised outputs; GELU within 1e-5 rel / 1e-6 abs)."""
+import contextlib
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -257,30 +260,62 @@ def test_fused_k64_layer_asymmetric_weights(gpu):
 
 # (M, N, K) choosing the 256x256, 128x256 and 128x128 block tiles on 256 CUs.
 GEMM_SHAPES = [(16384, 1024, 256), (8192, 1024, 128), (2000, 200, 192), (1, 64, 128), (500, 256, 320)]
+# Tile shapes forced through NFLOW_GEMM_TILE: "TM TN", a block tile of 32 TM x 32 TN outputs
+# (None: the launcher's choice).
+GEMM_TILES = [None, "22", "24", "44", "48", "88"]
 
 
+@contextlib.contextmanager
+def _env(**kv):
+    """Kernel-selection overrides (read by the library at each call)."""
+    old = {k: os.environ.get(k) for k in kv}
+    try:
+        for k, v in kv.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        yield
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.mark.parametrize("tile", GEMM_TILES)
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-def test_gemm_i32_tile_shapes(gpu, M, N, K):
+def test_gemm_i32_tile_shapes(gpu, M, N, K, tile):
     """int32 accumulators of every tile shape, bit-exact; the float64 product
     is exact here (|sum| <= K * 128^2 < 2^24)."""
     A = WL.uniform(30, (M, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
     W = WL.uniform(31, (N, K), -128, 128).astype(np.int64).clip(-128, 127).astype(np.int8)
     A[-1, :] = -128
     W[-1, :] = -128
-    got = _host(Q.gemm_i32(_cu(A), _cu(W)))
+    with _env(NFLOW_GEMM_TILE=tile):
+        got = _host(Q.gemm_i32(_cu(A), _cu(W)))
     want = (A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)
     assert np.array_equal(got, want)
 
 
+# The per-token layer's paths: "tiled" forces quantise + tiled GEMM where the
+# one-pass kernel (K = 128 / 256 / 512, N % 64 = 0) would take the shape.
+PATHS = {"auto": {}, "tiled": {"NFLOW_NO_TOKEN_GEMM": "1"}, "tiled22": {"NFLOW_NO_TOKEN_GEMM": "1",
+                                                                       "NFLOW_GEMM_TILE": "22"}}
+
+
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:3])
 @pytest.mark.parametrize("act", ["none", "gelu"])
-def test_gemm_per_token_layer_tile_shapes(gpu, M, N, K, act):
-    """The per-token layer through quantise + tiled GEMM, on sampled rows
-    (each output row depends only on its input row)."""
+def test_gemm_per_token_layer_tile_shapes(gpu, M, N, K, act, path):
+    """The per-token layer through quantise + tiled GEMM (or the one-pass
+    kernel), on sampled rows (each output row depends only on its input row)."""
     A = WL.normal(32, (M, K))
     _, q, s, zps, sw, b = _weights(N, K, 33)
     p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw))
-    out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
+    with _env(**PATHS[path]):
+        out, sa = Q.linear_forward_per_token(p, _cu(A), act, return_scales=True)
     out, sa = _host(out), _host(sa)
     rows = np.unique(np.concatenate([np.arange(0, M, 97), [M - 1]]))
     ref, sa_ref = O.layer_per_token_i8(A[rows], q, s, zps, b, sw, {"none": 0, "gelu": 2}[act])
@@ -291,10 +326,11 @@ def test_gemm_per_token_layer_tile_shapes(gpu, M, N, K, act):
         assert _bits_equal(out[rows], ref)
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("M,N,K", [(300, 256, 256), (70, 512, 1024), (9000, 1024, 128),
                                    (16384, 1024, 256), (8192, 1024, 128)])
 @pytest.mark.parametrize("with_sum", [False, True])
-def test_gemm_layer_asymmetric_weights(gpu, M, N, K, with_sum):
+def test_gemm_layer_asymmetric_weights(gpu, M, N, K, with_sum, path):
     """Zero points through the tiled GEMM: the row code sums and weight sums it
     accumulates feed LinearForward's formula (int8_gemm.cpp:386-393, 461-467)."""
     A = WL.normal(34, (M, K))
@@ -302,14 +338,16 @@ def test_gemm_layer_asymmetric_weights(gpu, M, N, K, with_sum):
     sumW = sw if with_sum else None
     p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b),
                            sum_W_per_row=None if sumW is None else _cu(sumW))
-    out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
+    with _env(**PATHS[path]):
+        out = _host(Q.linear_forward_per_token(p, _cu(A), "none"))
     rows = np.unique(np.concatenate([np.arange(0, M, 13), [M - 1]]))
     ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, 0)
     assert _bits_equal(out[rows], ref)
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("M,N,K", [(300, 256, 256), (16384, 1024, 320), (64, 1024, 1024)])
-def test_gemm_layer_given_sum_w_not_matching(gpu, M, N, K):
+def test_gemm_layer_given_sum_w_not_matching(gpu, M, N, K, path):
     """A caller-given sum_W_per_row that is not the weights' byte sum enters
     the row-VNNI formula verbatim (int8_gemm.cpp:386-393): the tiled GEMM must
     then form each column's own byte sum to reproduce it."""
@@ -317,7 +355,8 @@ def test_gemm_layer_given_sum_w_not_matching(gpu, M, N, K):
     _, q, s, zps, sw, b = _weights(N, K, 37)
     sw_bad = (sw + np.arange(N, dtype=np.int32) % 11 - 5).astype(np.int32)
     p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sw_bad))
-    out = _host(Q.linear_forward_per_token(p, _cu(A), "relu"))
+    with _env(**PATHS[path]):
+        out = _host(Q.linear_forward_per_token(p, _cu(A), "relu"))
     rows = np.unique(np.concatenate([np.arange(0, M, 17), [M - 1]]))
     ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sw_bad, 1)
     assert _bits_equal(out[rows], ref)
@@ -359,11 +398,8 @@ def test_token_gemm_layer(gpu, M, N, K, form, act):
         np.testing.assert_allclose(out[fin], ref[fin], rtol=RTOL, atol=ATOL)
     else:
         assert _bits_equal(out[fin], ref[fin])
-    os.environ["NFLOW_NO_TOKEN_GEMM"] = "1"
-    try:
+    with _env(NFLOW_NO_TOKEN_GEMM="1"):
         split = _host(Q.linear_forward_per_token(p, _cu(A), act))
-    finally:
-        del os.environ["NFLOW_NO_TOKEN_GEMM"]
     keep = ~np.isnan(split)
     assert np.array_equal(np.isnan(out), ~keep)
     assert _bits_equal(out[keep], split[keep])
