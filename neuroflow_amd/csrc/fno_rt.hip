@@ -466,11 +466,27 @@ __global__ __launch_bounds__(256) void k_spec_mix(SpecArgs a, const float* mix_r
     const float* Wr = mix_r + static_cast<int64_t>(m) * w * w + wo;
     const float* Wi = mix_i + static_cast<int64_t>(m) * w * w + wo;
     float sr = 0.0f, si = 0.0f;
-    for (int k = 0; k < w; ++k) {
-        const float2 hv = H[static_cast<int64_t>(k) * modes];
-        const float wr = Wr[static_cast<int64_t>(k) * w], wim = Wi[static_cast<int64_t>(k) * w];
-        sr = sr + __builtin_fmaf(-wim, hv.y, hv.x * wr);
-        si = si + __builtin_fmaf(wr, hv.y, hv.x * wim);
+    // The loads of 16 input channels are issued together (one at a time,
+    // each would wait out an L2 round trip); the sums still take the
+    // channels one by one, in order.
+    constexpr int KU = 16;
+    for (int k0 = 0; k0 < w; k0 += KU) {
+        float2 hv[KU];
+        float wr[KU], wim[KU];
+#pragma unroll
+        for (int j = 0; j < KU; ++j) {
+            const int k = k0 + j < w ? k0 + j : w - 1;    // clamped: only read, never summed
+            hv[j] = H[static_cast<int64_t>(k) * modes];
+            wr[j] = Wr[static_cast<int64_t>(k) * w];
+            wim[j] = Wi[static_cast<int64_t>(k) * w];
+        }
+#pragma unroll
+        for (int j = 0; j < KU; ++j) {
+            if (k0 + j < w) {
+                sr = sr + __builtin_fmaf(-wim[j], hv[j].y, hv[j].x * wr[j]);
+                si = si + __builtin_fmaf(wr[j], hv[j].y, hv[j].x * wim[j]);
+            }
+        }
     }
     reinterpret_cast<float2*>(spec_out)[(s * w + wo) * modes + m] = make_float2(sr, si);
 }
