@@ -47,6 +47,8 @@ def parse():
                     choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d", "fno2d"])
     ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay each step as a HIP graph (K = 64 workloads)")
     ap.add_argument("--check", action="store_true", default=True)
     ap.add_argument("--copy-calib", action="store_true",
                     help="also time a plain streaming kernel over the layer's bytes "
@@ -355,21 +357,54 @@ def main():
         sets.append(bufs)
     torch.cuda.synchronize()
 
-    def step(i):
+    def step(i, sp=sptr):
         bufs = sets[i % n_sets]
         for l, (_, run, L) in enumerate(layers):
             src = bufs[l] if wl.chained else bufs[0]
-            run(src.data_ptr(), bufs[l + 1].data_ptr(), M, sptr)
+            run(src.data_ptr(), bufs[l + 1].data_ptr(), M, sp)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+
+    # HIP graphs: one per buffer set, each the step's launches, replayed in
+    # the same rotation (the K = 64 path allocates nothing, so it captures).
+    graphs = None
+    if args.graph and all(L.W.shape[1] == 64 for L in wl.layers):
+        graphs = []
+        for k in range(n_sets):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step(k, torch.cuda.current_stream().cuda_stream)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        # Every replay equals the eager step: eager set 0, replay it twice
+        # with eager work between, compare the last output bit for bit.
+        last = sets[0][-1]
+        step(0)
+        torch.cuda.synchronize()
+        want = last.clone()
+        for _ in range(2):
+            last.fill_(float("nan"))
+            graphs[0].replay()
+            torch.cuda.synchronize()
+            if not torch.equal(last.view(torch.int32), want.view(torch.int32)):
+                raise RuntimeError("bench.py: a graph replay differs from the eager step")
+            step(1 % n_sets)
+            torch.cuda.synchronize()
+        for i in range(args.warmup):
+            graphs[i % n_sets].replay()
+        torch.cuda.synchronize()
+
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     ev0.record(stream)
     for i in range(args.steps):
-        step(i)
+        if graphs is not None:
+            graphs[i % n_sets].replay()
+        else:
+            step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1)
@@ -490,6 +525,7 @@ def main():
             "layers": [list(L.W.shape[::-1]) for L in wl.layers],
             "samples_per_step": wl.samples,
             "buffer_sets": n_sets,
+            "launch": "hip graph per step" if graphs is not None else "stream",
             "parallelism": "single GPU",
         },
         "roofline": roof,
