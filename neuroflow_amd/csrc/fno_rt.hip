@@ -8,7 +8,7 @@
 // (cpp/src/fno.cpp and fft.cpp compiled by g++ -O3 -mfma): products the
 // build fuses are written as __builtin_fmaf, everything else rounds on its
 // own (this library is compiled with -ffp-contract=off).  GELU is
-// gelu_ref (gelu_exact.h), bit-exact with glibc's tanhf.
+// gelu_fast (gelu_exact.h), bit-exact with glibc's tanhf.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -17,12 +17,13 @@
 #include "fno_rt.h"
 #include "gelu_exact.h"
 #include "launch.h"
+#include "snap.h"
 
 namespace nfq {
 
 __device__ __forceinline__ float rt_activate(float y, int act) {
     if (act == RT_ACT_RELU) return y < 0.0f ? 0.0f : y;  // fno.cpp:37-40
-    if (act == RT_ACT_GELU) return gelu_ref(y);
+    if (act == RT_ACT_GELU) return gelu_fast<kGeluRefine>(y);
     return y;
 }
 
@@ -213,6 +214,7 @@ __device__ __forceinline__ bool tile_of(int64_t id, int64_t samples, int n, int 
 // of each exponent from -5 to 9, computed on the host with that libm):
 // e = -6 + #{thr <= |v|} for 2^-6 <= |v| <= FLT_MAX; NaN and Inf give
 // ldexp(1, INT_MIN) = 0; 2^e for e >= 9 is capped at 448.
+template <bool BINADE = false>
 __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
     const float v = x / s;
     const float av = fabsf(v);
@@ -223,9 +225,7 @@ __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
     } else if (!(av <= 0x1.fffffep+127f)) {
         qv = 0.0f;
     } else {
-        int e = -6;
-#pragma unroll
-        for (int j = 0; j < 15; ++j) e += av >= thr[j] ? 1 : 0;
+        const int e = BINADE ? snap_exponent_binade(av, thr) : snap_exponent_count(av, thr);
         qv = e >= 9 ? 448.0f : __builtin_bit_cast(float, static_cast<uint32_t>(127 + e) << 23);
     }
     const float clamped = (448.0f < qv) ? 448.0f : qv;
@@ -555,9 +555,18 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
 // Layer tail.
 // ---------------------------------------------------------------------------
 
+// The snaps read their step tables from LDS, one entry per element
+// (snap_exponent_binade); the runtime checks the one-step-per-binade layout
+// of the table at creation.
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
     __shared__ float tx1[64][65];  // x1, then (in place, same thread) the new h
+    __shared__ float thr_x2[16], thr_next[16];
     const int n = a.n, w = a.w;
+    if (threadIdx.x < 15) {
+        thr_x2[threadIdx.x] = a.thr[threadIdx.x];
+        thr_next[threadIdx.x] = a.fq_next.thr[threadIdx.x];
+    }
+    __syncthreads();
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of(id, a.samples, n, w, tl); id += gridDim.x) {
         for (int i = threadIdx.x; i < 64 * 64; i += 256) {
@@ -576,9 +585,11 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
                     const int64_t p = static_cast<int64_t>(c) * n + t;
                     x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
                 } else if (a.kind == 3) {
-                    x2 = log2_snap(x2, a.scale, a.thr);
+                    x2 = log2_snap<true>(x2, a.scale, thr_x2);
                 }
-                const float hv = apply_fq(rt_activate(tx1[cr][tr] + x2, a.act), a.fq_next);
+                float hv = rt_activate(tx1[cr][tr] + x2, a.act);
+                if (a.fq_next.on == 1) hv = x2_fake_quant(hv, a.fq_next.scale, a.fq_next.zpf);
+                else if (a.fq_next.on == 3) hv = log2_snap<true>(hv, a.fq_next.scale, thr_next);
                 a.h[o] = hv;
                 tx1[cr][tr] = hv;
             }

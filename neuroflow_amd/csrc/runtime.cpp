@@ -31,6 +31,7 @@
 #include "fno_rt.h"
 #include "nflow_quant.h"
 #include "nflow_runtime.h"
+#include "snap.h"
 #include "status.h"
 
 namespace nfq {
@@ -426,6 +427,8 @@ int init(nflow_runtime* rt) {
     }
     if (any_snap && !snap_thresholds(rt->thr))
         return set_error(NFLOW_INTERNAL, "runtime: the host libm's log2 is not monotone at a snap step");
+    if (any_snap && !nfq::snap_table_binned(rt->thr))
+        return set_error(NFLOW_INTERNAL, "runtime: a snap step of the host libm lies outside its binade");
     for (FakeQuant* f : {&rt->fq_lift, &rt->fq_projq, &rt->fq_projout})
         std::memcpy(f->thr, rt->thr, sizeof(f->thr));
 
