@@ -212,9 +212,9 @@ __device__ __forceinline__ bool tile_of(int64_t id, int64_t samples, int n, int 
 // fno.cpp:579-606 with the exponent e = int(std::round(log2|v| * 8) / 8)
 // read off the step points of the reference's libm (thr: the smallest float
 // of each exponent from -5 to 9, computed on the host with that libm):
-// e = -6 + #{thr <= |v|} for 2^-6 <= |v| <= FLT_MAX; NaN and Inf give
-// ldexp(1, INT_MIN) = 0; 2^e for e >= 9 is capped at 448.
-template <bool BINADE = false>
+// e = -6 + #{thr <= |v|} for 2^-6 <= |v| <= FLT_MAX, taken from |v|'s binade
+// and one compare (snap.h; thr in LDS); NaN and Inf give ldexp(1, INT_MIN)
+// = 0; 2^e for e >= 9 is capped at 448.
 __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
     const float v = x / s;
     const float av = fabsf(v);
@@ -225,29 +225,39 @@ __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
     } else if (!(av <= 0x1.fffffep+127f)) {
         qv = 0.0f;
     } else {
-        const int e = BINADE ? snap_exponent_binade(av, thr) : snap_exponent_count(av, thr);
+        const int e = snap_exponent_binade(av, thr);
         qv = e >= 9 ? 448.0f : __builtin_bit_cast(float, static_cast<uint32_t>(127 + e) << 23);
     }
     const float clamped = (448.0f < qv) ? 448.0f : qv;
     return (sign * clamped) * s;
 }
 
-__device__ __forceinline__ float apply_fq(float v, const FakeQuant& q) {
+// The activation fake-quant q, the snap's step table read from LDS
+// (stage_steps), one entry per element (snap_exponent_binade).
+__device__ __forceinline__ float apply_fq_lds(float v, const FakeQuant& q, const float* steps) {
     if (q.on == 1) return x2_fake_quant(v, q.scale, q.zpf);
-    if (q.on == 3) return log2_snap(v, q.scale, q.thr);
+    if (q.on == 3) return log2_snap(v, q.scale, steps);
     return v;
+}
+
+// Copies a step table into LDS; every thread of the block must call it.
+__device__ __forceinline__ void stage_steps(float* steps, const float* thr) {
+    if (threadIdx.x < 15) steps[threadIdx.x] = thr[threadIdx.x];
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, int64_t samples, int n, int w,
                                                           FakeQuant fq) {
     __shared__ float tile[64][65];
+    __shared__ float steps[16];
+    stage_steps(steps, fq.thr);
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of(id, samples, n, w, tl); id += gridDim.x) {
         for (int i = threadIdx.x; i < 64 * 64; i += 256) {
             const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) {
                 const int64_t o = (tl.s * n + t) * w + c;
-                const float v = apply_fq(h[o], fq);
+                const float v = apply_fq_lds(h[o], fq, steps);
                 if (fq.on != 0) h[o] = v;
                 tile[cr][tr] = v;
             }
@@ -562,11 +572,8 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
     __shared__ float tx1[64][65];  // x1, then (in place, same thread) the new h
     __shared__ float thr_x2[16], thr_next[16];
     const int n = a.n, w = a.w;
-    if (threadIdx.x < 15) {
-        thr_x2[threadIdx.x] = a.thr[threadIdx.x];
-        thr_next[threadIdx.x] = a.fq_next.thr[threadIdx.x];
-    }
-    __syncthreads();
+    if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
+    stage_steps(thr_next, a.fq_next.thr);
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of(id, a.samples, n, w, tl); id += gridDim.x) {
         for (int i = threadIdx.x; i < 64 * 64; i += 256) {
@@ -585,11 +592,9 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
                     const int64_t p = static_cast<int64_t>(c) * n + t;
                     x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
                 } else if (a.kind == 3) {
-                    x2 = log2_snap<true>(x2, a.scale, thr_x2);
+                    x2 = log2_snap(x2, a.scale, thr_x2);
                 }
-                float hv = rt_activate(tx1[cr][tr] + x2, a.act);
-                if (a.fq_next.on == 1) hv = x2_fake_quant(hv, a.fq_next.scale, a.fq_next.zpf);
-                else if (a.fq_next.on == 3) hv = log2_snap<true>(hv, a.fq_next.scale, thr_next);
+                const float hv = apply_fq_lds(rt_activate(tx1[cr][tr] + x2, a.act), a.fq_next, thr_next);
                 a.h[o] = hv;
                 tx1[cr][tr] = hv;
             }
@@ -629,8 +634,10 @@ __global__ __launch_bounds__(256) void k_pad2d(const float* src, float* dst, int
 }
 
 __global__ __launch_bounds__(256) void k_fq_act(float* y, int64_t n, FakeQuant fq, int act) {
+    __shared__ float steps[16];
+    stage_steps(steps, fq.thr);
     for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
-        y[i] = rt_activate(apply_fq(y[i], fq), act);
+        y[i] = rt_activate(apply_fq_lds(y[i], fq, steps), act);
 }
 
 // ---------------------------------------------------------------------------
