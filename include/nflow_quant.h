@@ -93,6 +93,16 @@ int nflow_quant_abi_version(void);
 /* Message of the last non-OK status returned on this thread ("" if none). */
 const char* nflow_last_error(void);
 
+/* Kernel-path override for A/B timing and for tests that pin one of two
+ * kernels computing the same bits (no counterpart in the reference, whose
+ * SIMD path is fixed at compile time, int8_gemm.cpp:34-45).  Names:
+ * "no_gemm", "no_rows64", "no_token_gemm", "gemm_reg" (0 / 1) and
+ * "gemm_tile" (0 = the launcher's choice, else 88, 48, 44, 24 or 22).  The
+ * environment variables NFLOW_<NAME> set the initial values, read once at
+ * the library's first launch.  Process-wide; *previous (if not NULL)
+ * receives the value replaced.  Unknown names return NFLOW_INVALID_ARG. */
+int nflow_debug_set_kernel_path(const char* name, int value, int* previous);
+
 /* ---- nflow-quant kernel API (cpp/include/neuroflow/int8_gemm.h) ------------ */
 
 /* Replaces int8_gemm::QuantiseActivation (int8_gemm.h:115-118,

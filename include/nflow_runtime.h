@@ -14,8 +14,12 @@
  * callers, a header-only nflow::InferenceRuntime with the reference's
  * signatures over this C-ABI.
  *
- * A runtime handle is used by one thread at a time; creation uploads the
- * weights to the current device, runs use that device.
+ * Creation uploads the weights to the current device; runs use that device.
+ * Runs, EnableInt8Gemm and the queries may be called from several threads:
+ * a per-handle lock serialises them on the host, and a run enqueued on a
+ * different stream than the handle's previous run first waits (an event)
+ * for that run, because the runs of one handle share its device workspace.
+ * Destroying a handle while another thread uses it is the caller's error.
  */
 #ifndef NFLOW_RUNTIME_H
 #define NFLOW_RUNTIME_H

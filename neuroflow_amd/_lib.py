@@ -77,6 +77,7 @@ _PF8 = C.POINTER(Fp8LinearParamsC)
 SIGNATURES = {
     "nflow_quant_abi_version": [],
     "nflow_last_error": [],
+    "nflow_debug_set_kernel_path": [C.c_char_p, _i32, C.POINTER(C.c_int)],
     "nflow_int8_quantise_activation": [_vp, _vp, _i64, _i32, _f32, C.c_int32, _vp],
     "nflow_int8_precompute_sum_w": [_vp, _vp, _i32, _i32, _vp, _vp],
     "nflow_int8_linear_forward": [_P8, _vp, _vp, _vp],

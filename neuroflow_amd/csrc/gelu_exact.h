@@ -3,7 +3,7 @@
 // fno.cpp:41-46 evaluates 0.5f * z * (1 + std::tanh(c * (z + 0.044715f z^3)))
 // with glibc's tanhf; its build (g++ -O3 -mfma) fuses the last product of the
 // cubic term with the addition.  glibc's float tanhf and expm1f are the
-// fdlibm algorithms (Sun Microsystems, freely distributable): tanhf from
+// fdlibm algorithms (s_tanhf.c, s_expm1f.c; notice below): tanhf from
 // expm1f of 2|x|, expm1f by argument reduction x = k ln2 + r and a rational
 // approximation in r^2 with the published coefficients below.  This
 // restatement reproduces glibc 2.35's tanhf on every one of the 2^32 float
@@ -12,6 +12,22 @@
 // build of this library do.
 //
 // Usable from host code (the test harness) and device code.
+//
+// expm1f_fdlibm and tanhf_fdlibm below follow fdlibm's s_expm1f.c and
+// s_tanhf.c (their thresholds, coefficients and control flow), which carry
+// this notice:
+//
+// ====================================================
+// Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+// Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this
+// software is freely granted, provided that this notice
+// is preserved.
+// ====================================================
+//
+// (The float versions: conversion to float by Ian Lance Taylor, Cygnus
+// Support, ian@cygnus.com.)
 #pragma once
 
 #include <stdint.h>

@@ -31,12 +31,10 @@ static void launch_gemm_t(const RowsArgs& a, hipStream_t st) {
 // else 128 x 128.  Measured on MI355X: 256 x 256 (one wave per SIMD) never
 // beats 128 x 256, 64 x 128 loses at the trunk (173 us against 139 us).
 static int gemm_shape(const RowsArgs& a) {
-    // NFLOW_GEMM_TILE=88|48|44|24|22 forces a shape (for tile sweeps; 22 and 24 only
-    // on the LDS-DMA kernel).
-    if (const char* f = std::getenv("NFLOW_GEMM_TILE")) {
-        const int t = std::atoi(f);
-        if (t == 88 || t == 48 || t == 44 || t == 22 || t == 24) return t;
-    }
+    // A gemm_tile override of 88|48|44|24|22 forces a shape (for tile sweeps;
+    // 22 and 24 only on the LDS-DMA kernel).
+    const int t = kernel_path().gemm_tile.load(std::memory_order_relaxed);
+    if (t == 88 || t == 48 || t == 44 || t == 22 || t == 24) return t;
     if (a.M >= 16384 && a.N >= 1024) return 48;
     return (a.M <= 4096 && a.N >= 512) ? 24 : 44;
 }
@@ -54,7 +52,7 @@ static void launch_pipe_t(const RowsArgs& a, hipStream_t st) {
 // its own: zp_A = 0, row sums given when zero points may be nonzero, and
 // weight-row sums given when the row-VNNI formula has a caller's sum_W.
 bool gemm_pipe_ok(const RowsArgs& a, int out) {
-    if (a.zp_A != 0 || getenv_flag("NFLOW_GEMM_REG")) return false;
+    if (a.zp_A != 0 || path_flag(kernel_path().gemm_reg)) return false;
     if (out == OUT_RAW) return true;
     const bool need_colsum = a.formula == F_ROW_VNNI && a.sumW;
     return (!a.zpW || a.sum_in) && (!need_colsum || a.colsum_in);

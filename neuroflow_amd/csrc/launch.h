@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
@@ -40,12 +41,22 @@ inline unsigned grid_for(int64_t work_items, int64_t per_block, int max_blocks_p
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// A kernel-selection override read at each call (for A/B comparisons of
-// two kernels that compute the same bits).
-inline bool getenv_flag(const char* name) {
-    const char* v = std::getenv(name);
-    return v && v[0] && v[0] != '0';
-}
+// Kernel-selection overrides, for A/B timing and for tests that pin one of
+// two kernels computing the same bits.  They are read from the environment
+// once, at the first launch (NFLOW_NO_GEMM, NFLOW_NO_ROWS64,
+// NFLOW_NO_TOKEN_GEMM, NFLOW_GEMM_REG, NFLOW_GEMM_TILE), and afterwards
+// change only through nflow_debug_set_kernel_path; a launch reads relaxed
+// atomics, never the environment.
+struct KernelPath {
+    std::atomic<int> no_gemm{0};
+    std::atomic<int> no_rows64{0};
+    std::atomic<int> no_token_gemm{0};
+    std::atomic<int> gemm_reg{0};
+    std::atomic<int> gemm_tile{0};   // 0: the launcher's choice
+};
+KernelPath& kernel_path();
+
+inline bool path_flag(const std::atomic<int>& f) { return f.load(std::memory_order_relaxed) != 0; }
 
 inline bool aligned(const void* p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;

@@ -389,6 +389,25 @@ static void launch_quantise_token(const float* A, int64_t M, int K, uint8_t* Aq,
     hipLaunchKernelGGL((k_quantise_token<FP8>), grid, block, 0, st, A, M, K, Aq, scale, sum_a, cs);
 }
 
+static int env_int(const char* name) {
+    const char* v = std::getenv(name);
+    return (v && v[0]) ? std::atoi(v) : 0;
+}
+
+// Initialised from the environment on first use (a thread-safe static).
+KernelPath& kernel_path() {
+    static KernelPath* k = [] {
+        auto* p = new KernelPath();
+        p->no_gemm.store(env_int("NFLOW_NO_GEMM"));
+        p->no_rows64.store(env_int("NFLOW_NO_ROWS64"));
+        p->no_token_gemm.store(env_int("NFLOW_NO_TOKEN_GEMM"));
+        p->gemm_reg.store(env_int("NFLOW_GEMM_REG"));
+        p->gemm_tile.store(env_int("NFLOW_GEMM_TILE"));
+        return p;
+    }();
+    return *k;
+}
+
 static int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(NFLOW_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
@@ -448,7 +467,7 @@ static int int8_fixed_path(const nflow_int8_linear_params* p, int64_t rows, cons
 
 // The tiled GEMM serves INT8 code input with K a multiple of 64, K >= 128
 // (NFLOW_NO_GEMM=1 selects the row-tile kernel instead, for A/B timing).
-static bool use_gemm(const RowsArgs& a) { return gemm_ok(a) && !getenv_flag("NFLOW_NO_GEMM"); }
+static bool use_gemm(const RowsArgs& a) { return gemm_ok(a) && !path_flag(kernel_path().no_gemm); }
 
 static int check_params(const nflow_int8_linear_params* p, const char* what) {
     if (!p || !p->W_int8 || !p->scale_W || !p->zp_W)
@@ -467,6 +486,22 @@ using namespace nfq;
 extern "C" {
 
 int nflow_quant_abi_version(void) { return NFLOW_QUANT_ABI_VERSION; }
+
+int nflow_debug_set_kernel_path(const char* name, int value, int* previous) {
+    clear_error();
+    if (!name) return set_error(NFLOW_INVALID_ARG, "debug_set_kernel_path: null name");
+    KernelPath& k = kernel_path();
+    const std::string n(name);
+    std::atomic<int>* f = n == "no_gemm" ? &k.no_gemm
+                        : n == "no_rows64" ? &k.no_rows64
+                        : n == "no_token_gemm" ? &k.no_token_gemm
+                        : n == "gemm_reg" ? &k.gemm_reg
+                        : n == "gemm_tile" ? &k.gemm_tile : nullptr;
+    if (!f) return set_error(NFLOW_INVALID_ARG, "debug_set_kernel_path: unknown name " + n);
+    const int old = f->exchange(value, std::memory_order_relaxed);
+    if (previous) *previous = old;
+    return NFLOW_OK;
+}
 
 int nflow_int8_quantise_activation(const float* A, int8_t* A_q, int64_t bsz, int in_features,
                                    float scale_A, int32_t zp_A, void* stream) {
@@ -592,7 +627,7 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
     a.kb_dot = kb_dot_for(a.formula, a.K);
     a.C = C;
     a.scale_out = scale_A_out;
-    if (rows64_ok(a) && (!R || aligned(R, 16)) && !getenv_flag("NFLOW_NO_ROWS64")) {
+    if (rows64_ok(a) && (!R || aligned(R, 16)) && !path_flag(kernel_path().no_rows64)) {
         a.residual = R;
         launch_rows64<false>(a, activation, st);
         return check_launch("linear_forward_per_token");
@@ -604,7 +639,7 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
         return check_launch("linear_forward_per_token");
     };
     // K = 128 .. 512: the one-pass kernel (quantise into LDS, then all of N).
-    if (token_gemm_ok(a) && !getenv_flag("NFLOW_NO_TOKEN_GEMM")) {
+    if (token_gemm_ok(a) && !path_flag(kernel_path().no_token_gemm)) {
         launch_token_gemm(a, act_x2, st);
         return finish();
     }
@@ -806,7 +841,7 @@ static int fp8_per_token(const nflow_fp8_linear_params* p, int64_t M, const floa
     a.kb_dot = (a.K + 63) / 64;
     a.C = C;
     a.scale_out = scale_A_out;
-    if (rows64_ok(a) && (!R || aligned(R, 16)) && !getenv_flag("NFLOW_NO_ROWS64")) {
+    if (rows64_ok(a) && (!R || aligned(R, 16)) && !path_flag(kernel_path().no_rows64)) {
         a.residual = R;
         launch_rows64<true>(a, activation, st);
         return check_launch("fp8_linear_forward_per_token");

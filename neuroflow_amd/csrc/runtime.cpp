@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -193,6 +194,16 @@ struct nflow_runtime {
     void* ws = nullptr;
     size_t ws_bytes = 0;
 
+    // Runs on one handle share the tables and the workspace above.  `mu`
+    // serialises the host side (table inserts, workspace growth, the INT8
+    // cache); `done` is recorded on the stream of every run, and a run on a
+    // different stream than the previous one first waits for it, so two runs
+    // never use the workspace at the same time on the device.
+    std::mutex mu;
+    hipStream_t last_stream = nullptr;
+    hipEvent_t done = nullptr;
+    bool ran = false;
+
     const float* dw(const std::string& name) const {
         return static_cast<const float*>(dblock) + off.at(name);
     }
@@ -211,6 +222,7 @@ void free_runtime(nflow_runtime* rt) {
     for (auto& kv : rt->zfill) (void)hipFree(kv.second);
     if (rt->dblock) (void)hipFree(rt->dblock);
     if (rt->ws) (void)hipFree(rt->ws);
+    if (rt->done) (void)hipEventDestroy(rt->done);
     if (sw) (void)hipSetDevice(cur);
     if (rt->ir) nflow_ir_close(rt->ir);
     delete rt;
@@ -801,6 +813,26 @@ struct DeviceGuard {
     }
 };
 
+// Orders a run on `st` after the handle's previous run (called with rt->mu
+// held) and, once the run is enqueued, marks its end.
+int order_run(nflow_runtime* rt, hipStream_t st) {
+    if (!rt->done && hipEventCreateWithFlags(&rt->done, hipEventDisableTiming) != hipSuccess) {
+        rt->done = nullptr;
+        return set_error(NFLOW_INTERNAL, "runtime_run: event creation failed");
+    }
+    if (rt->ran && st != rt->last_stream && hipStreamWaitEvent(st, rt->done, 0) != hipSuccess)
+        return set_error(NFLOW_INTERNAL, "runtime_run: cross-stream wait failed");
+    return NFLOW_OK;
+}
+
+int mark_run(nflow_runtime* rt, hipStream_t st, int rc) {
+    if (rc) return rc;
+    if (hipEventRecord(rt->done, st) != hipSuccess) return set_error(NFLOW_INTERNAL, "runtime_run: event record failed");
+    rt->last_stream = st;
+    rt->ran = true;
+    return NFLOW_OK;
+}
+
 int create_from(nflow_ir* ir, nflow_runtime** out) {
     nflow_runtime* rt = new (std::nothrow) nflow_runtime;
     if (!rt) {
@@ -905,6 +937,7 @@ int nflow_runtime_enable_int8_gemm(nflow_runtime* rt) {
     if (!rt) return set_error(NFLOW_INVALID_ARG, "runtime_enable_int8_gemm: null runtime");
     // runtime.cpp:155-166: a no-op for every model but FNO1d.
     if (rt->fno2d) return NFLOW_OK;
+    std::lock_guard<std::mutex> lock(rt->mu);
     return build_int8_layers(rt);
 }
 
@@ -914,6 +947,7 @@ int nflow_runtime_enable_int8_gemm_fno2d(nflow_runtime* rt) {
     if (!rt->fno2d)
         return set_error(NFLOW_UNSUPPORTED_OP, "runtime_enable_int8_gemm_fno2d: the model is " + rt->op +
                                                    " (FNO1d has EnableInt8Gemm)");
+    std::lock_guard<std::mutex> lock(rt->mu);
     return build_int8_layers(rt);
 }
 
@@ -940,8 +974,11 @@ int nflow_runtime_run_device(nflow_runtime* rt, const float* x, const int64_t* x
     if (int rc = check_shapes(rt, x_shape, x_ndim, y_shape, y_ndim)) return rc;
     if (x_shape[0] > 0 && (!x || !y)) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
     DeviceGuard g(rt->device);
-    if (rt->fno2d) return run_device_2d(rt, x, x_shape, y, static_cast<hipStream_t>(stream));
-    return run_device(rt, x, x_shape, y, static_cast<hipStream_t>(stream));
+    std::lock_guard<std::mutex> lock(rt->mu);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (int rc = order_run(rt, st)) return rc;
+    const int rc = rt->fno2d ? run_device_2d(rt, x, x_shape, y, st) : run_device(rt, x, x_shape, y, st);
+    return mark_run(rt, st, rc);
 }
 
 int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape, int x_ndim, float* y,
@@ -963,8 +1000,11 @@ int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape,
         return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
     }
     int rc = NFLOW_OK;
+    std::unique_lock<std::mutex> lock(rt->mu);
     if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
-    if (!rc) rc = rt->fno2d ? run_device_2d(rt, dx, x_shape, dy, nullptr) : run_device(rt, dx, x_shape, dy, nullptr);
+    if (!rc) rc = order_run(rt, nullptr);
+    if (!rc) rc = mark_run(rt, nullptr, rt->fno2d ? run_device_2d(rt, dx, x_shape, dy, nullptr)
+                                                  : run_device(rt, dx, x_shape, dy, nullptr));
     if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess)
         rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
     if (!rc && hipDeviceSynchronize() != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: device error");

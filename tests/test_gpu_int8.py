@@ -1,12 +1,13 @@
 """GPU parity of the INT8 path against the oracle (bit-exact codes, int32
 accumulators and dequantised outputs; GELU within 1e-5 rel / 1e-6 abs)."""
 import contextlib
-import os
+import ctypes
 
 import numpy as np
 import pytest
 import torch
 
+from neuroflow_amd import _lib
 from neuroflow_amd import quant as Q
 from neuroflow_amd import workloads as WL
 from oracle import oracle as O
@@ -267,21 +268,22 @@ GEMM_TILES = [None, "22", "24", "44", "48", "88"]
 
 @contextlib.contextmanager
 def _env(**kv):
-    """Kernel-selection overrides (read by the library at each call)."""
-    old = {k: os.environ.get(k) for k in kv}
+    """Kernel-selection overrides through nflow_debug_set_kernel_path
+    (NFLOW_NO_TOKEN_GEMM="1" -> "no_token_gemm" = 1, NFLOW_GEMM_TILE="22" ->
+    "gemm_tile" = 22; None -> 0), restored afterwards."""
+    L = _lib.lib()
+    old = {}
     try:
         for k, v in kv.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
+            name = k[len("NFLOW_"):].lower().encode()
+            prev = ctypes.c_int(0)
+            _lib.check(L.nflow_debug_set_kernel_path(name, int(v) if v is not None else 0, ctypes.byref(prev)),
+                       "debug_set_kernel_path")
+            old[name] = prev.value
         yield
     finally:
-        for k, v in old.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
+        for name, v in old.items():
+            _lib.check(L.nflow_debug_set_kernel_path(name, v, None), "debug_set_kernel_path")
 
 
 @pytest.mark.parametrize("tile", GEMM_TILES)
