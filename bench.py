@@ -19,7 +19,16 @@ launch are 4MK + 4MN + NK*b_w + 8N and its duration is the timed region
 divided by the number of launches.  The CPU baseline is the reference's own
 INT8 kernel (int8_gemm::LinearForward, AVX-512 VNNI build from oracle/_ref)
 called once per row with that row's scale, plus the tanh GELU, on the host's
-cores, over a bounded sample of the same rows.
+cores, over a bounded sample of the same rows; the line also carries
+LinearForwardBatched (the FNO1d runtime's path) and, for FP8, the reference
+codec's fake-quant + fp32 loop.
+
+Parity: the outputs of the last timed step (every layer, on the input it
+read) are compared with the oracle on sampled rows (oracle/parity.py).
+
+By default every other configuration (C1, C3, C4, C5 trunk / branch) is
+measured the same way after the headline one and reported under "configs",
+each with its kernel time, roofline fraction, parity and a CPU figure.
 """
 from __future__ import annotations
 
@@ -47,9 +56,13 @@ def parse():
                     choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d", "fno2d"])
     ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="measure only --workload (by default every other configuration is measured "
+                         "too and reported under \"configs\")")
     ap.add_argument("--graph", action="store_true",
                     help="replay each step as a HIP graph (K = 64 workloads)")
-    ap.add_argument("--check", action="store_true", default=True)
+    ap.add_argument("--no-check", dest="check", action="store_false",
+                    help="skip the oracle parity of the timed step's outputs")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also time a plain streaming kernel over the layer's bytes "
                          "(torch.neg: read M*N*4, write M*N*4): the achievable-bandwidth "
@@ -82,14 +95,16 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     needs no byte sums and runs the same LDS-DMA kernel as the layer, with
     identical outputs."""
     import ctypes as C
+    import dataclasses
+
     import torch
     from neuroflow_amd import _lib
     from neuroflow_amd import quant as Q
     obj, _, L = layers[0]
     M, N = wl.M, L.W.shape[0]
-    codes = [Q.quantise_per_token(s_[0]) for s_ in sets]
-    outs = [torch.empty(M, N, dtype=torch.float32, device=sets[0][0].device) for _ in sets]
-    import dataclasses
+    kind, k = wl.source(0)
+    codes = [Q.quantise_per_token(s_["in"][k]) for s_ in sets]
+    outs = [torch.empty(M, N, dtype=torch.float32, device=sets[0]["in"][0].device) for _ in sets]
     assert not obj.params.zp_W.any().item()
     ps = dataclasses.replace(obj.params, zp_W=None, sum_W_per_row=None).c_struct()
     fn = _lib.lib().nflow_int8_linear_forward_quantised
@@ -125,54 +140,274 @@ def build_layers(wl, dev):
     return layers
 
 
-def cpu_baseline(wl, layers, args):
-    """Reference kernel on the host cores over a bounded sample of rows."""
+def _cpu_rows(K, N, ops_log2):
+    """Rows of a K x N layer holding about 2^ops_log2 multiply-adds."""
+    return max(256, (1 << ops_log2) // (K * N))
+
+
+def cpu_baseline(wl, layers, legs=("token",), budget_log2=32):
+    """The reference kernel on the host cores over a bounded sample of the
+    workload's layer-0 rows (about 2^budget_log2 multiply-adds on all cores,
+    a quarter of that on one), scaled to samples/s of the whole step (the
+    step's layers weighted by their multiply-adds).
+
+    Legs (the reference has no batched per-token entry point and no FP8 GEMM):
+      token    int8_gemm::LinearForward once per row with scale_A = absmax/127
+               (int8_gemm.cpp:201-470), + tanh GELU -- the per-token path;
+      batched  int8_gemm::LinearForwardBatched with one per-tensor scale
+               (int8_gemm.cpp:530-580) -- what FNO1d's runtime runs;
+      fp8      per-row fp8_e4m3_per_tensor_fake_quant (fp8_e4m3.h:312-334) +
+               the fp32 Linear loop (fno.cpp:68-79) + GELU.
+    """
     import numpy as np
     from oracle import oracle as O
 
     L0 = wl.layers[0]
     obj = layers[0][0]
+    N, K = L0.W.shape
     cores = O.usable_cores()
-    M_all = wl.M
-    total_rows = M_all * len(wl.layers)          # rows of one step
     variant = O.ref_variant()
-    if L0.fmt == "int8" and variant is not None and O.ref_available(variant):
-        gelu = L0.act == "gelu"
-        n1 = min(M_all, 16384)
-        t1, _ = O.ref_time_per_token_layer(wl.x[:n1], obj.W_q, obj.scale_W, L0.bias, obj.sum_W,
-                                           threads=1, reps=3, act_gelu=gelu, variant=variant)
-        nN = min(M_all, 262144)
-        tN, _ = O.ref_time_per_token_layer(wl.x[:nN], obj.W_q, obj.scale_W, L0.bias, obj.sum_W,
-                                           threads=cores, reps=3, act_gelu=gelu, variant=variant)
-        rows_s_1, rows_s_N = n1 / t1, nN / tN
-        kind = "reference"
-        sample = (f"int8_gemm::LinearForward ({variant.upper()} build of the reference "
-                  f"sources) once per row with scale_A = absmax/127 + tanh GELU, layer 0 "
-                  f"(K={L0.W.shape[1]}, N={L0.W.shape[0]}): {nN} rows x 3 reps on {cores} "
-                  f"threads, {n1} rows x 3 reps on 1 thread; host {O.host_cpu_model()}")
+    if variant is None or not O.ref_available(variant):
+        raise RuntimeError("oracle/_ref (the reference build) is not available on this host")
+    step_row_layers = sum(wl.M * wl.layers[l].W.shape[0] * wl.layers[l].W.shape[1]
+                          for l in range(len(wl.layers))) / (K * N)   # layer-0-equivalent rows per step
+    to_samples = wl.samples / step_row_layers
+    x0 = wl.inputs[wl.source(0)[1]]
+    nN = min(wl.M, _cpu_rows(K, N, budget_log2))
+    n1 = min(wl.M, _cpu_rows(K, N, budget_log2 - 2))
+    gelu = L0.act == "gelu"
+    out = {"unit": "samples/s", "cores": cores, "kind": "reference", "host": O.host_cpu_model(),
+           "legs": {}}
+    for leg in legs:
+        rates = {}
+        for threads, n in ((1, n1), (cores, nN)):
+            if leg == "token":
+                t, _ = O.ref_time_per_token_layer(x0[:n], obj.W_q, obj.scale_W, L0.bias, obj.sum_W,
+                                                  threads=threads, reps=3, act_gelu=gelu, variant=variant)
+            elif leg == "batched":
+                s_a = float(np.float32(np.abs(x0[:n]).max()) / np.float32(127.0))
+                t, _ = O.ref_time_batched_layer(x0[:n], obj.W_q, obj.scale_W, L0.bias, obj.sum_W, s_a,
+                                                threads=threads, reps=3, variant=variant)
+            else:
+                t, _ = O.ref_time_fp8_layer(x0[:n], L0.W, L0.bias, threads=threads, reps=3, act_gelu=gelu,
+                                            variant=variant)
+            rates[threads] = n / t
+        desc = {"token": "int8_gemm::LinearForward once per row with scale_A = absmax/127 "
+                         "(the per-token path)" + (" + tanh GELU" if gelu else ""),
+                "batched": "int8_gemm::LinearForwardBatched, one per-tensor scale (FNO1d's runtime "
+                           "path; no GELU)",
+                "fp8": "per-row fp8_e4m3_per_tensor_fake_quant + fp32 Linear loop"
+                       + (" + tanh GELU" if gelu else "") + " (the reference has no FP8 GEMM)"}[leg]
+        out["legs"][leg] = {"value": rates[cores] * to_samples, "value_1core": rates[1] * to_samples,
+                            "rows_per_s": rates[cores], "rows_per_s_1core": rates[1],
+                            "sample": f"{desc}: layer 0 (K={K}, N={N}), {nN} rows x 3 reps on {cores} threads, "
+                                      f"{n1} rows x 3 reps on 1 thread, median"}
+    first = out["legs"][legs[0]]
+    out.update({"value": first["value"], "value_1core": first["value_1core"],
+                "sample": first["sample"] + f"; {variant.upper()} build of the reference sources; host "
+                                            f"{out['host']}"})
+    return out
+
+
+def _kernel_of(wl):
+    N0, K0 = wl.layers[0].W.shape
+    if K0 == 64 and N0 == 64:
+        return "nfq::k_rows64"
+    if (wl.layers[0].fmt == "int8" and all(l.W.shape[1] in (128, 256, 512) and l.W.shape[0] % 64 == 0
+                                           for l in wl.layers)):
+        return "nfq::k_token_gemm"    # the whole per-token layer in one launch
+    if K0 % 64 == 0 and K0 >= 128 and wl.layers[0].fmt == "int8":
+        return "nfq::k_gemm_pipe"     # after a per-token quantise launch
+    return "nfq::k_rows"
+
+
+def check_timed_step(wl, layers, bufs):
+    """Oracle parity of every layer output of one timed step (sampled rows;
+    layer l is checked on the input it read in that step)."""
+    import torch
+    from oracle import parity as P
+
+    res = []
+    for l, (obj, _, L) in enumerate(layers):
+        kind, k = wl.source(l)
+        x = bufs["in"][k] if kind == "input" else bufs["out"][k]
+        y = bufs["out"][l]
+        N, K = L.W.shape
+        rows = P.sample_rows(wl.M, K, N)
+        idx = torch.from_numpy(rows).to(x.device)
+        x_rows = x.index_select(0, idx).cpu().numpy()
+        got = y.index_select(0, idx).cpu().numpy()
+        want, _ = P.layer_ref(L.fmt, obj.W_q, obj.scale_W, getattr(obj, "sum_W", None), L.bias, x_rows, L.act)
+        r = P.compare(got, want, L.fmt, L.act)
+        res.append(r)
+    return {"ok": all(r["ok"] for r in res), "layers": len(res), "rows_per_layer": [r["rows"] for r in res],
+            "bit_exact_frac_min": round(min(r["bit_exact_frac"] for r in res), 6),
+            "max_abs_diff": max(r["max_abs"] for r in res),
+            "bar": "INT8: bit-exact without GELU, 1e-5 rel / 1e-6 abs with GELU; FP8: 1e-5 / 1e-6 of the "
+                   "exact-product oracle"}
+
+
+def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, graph=False):
+    """Times `steps` steps of workload `name` (after `warmup`) and returns its
+    measurement record."""
+    import torch
+    from neuroflow_amd import workloads as WL
+
+    dev = torch.device("cuda:0")
+    t_gen = time.perf_counter()
+    wl = WL.WORKLOADS[name]()
+    t_gen = time.perf_counter() - t_gen
+    layers = build_layers(wl, dev)
+    M = wl.M
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+
+    # Buffer sets (the inputs and one output per layer), rotated across steps
+    # so that a step's input is not resident in the 256 MB last-level cache.
+    set_bytes = sum(x.nbytes for x in wl.inputs) + sum(4 * M * L.W.shape[0] for L in wl.layers)
+    n_sets = args.sets or max(2, min(8, -(-1_100_000_000 // set_bytes)))
+    host_in = [torch.from_numpy(x) for x in wl.inputs]
+    sets = []
+    for _ in range(n_sets):
+        sets.append({"in": [h.to(dev) for h in host_in],
+                     "out": [torch.empty(M, L.W.shape[0], dtype=torch.float32, device=dev) for L in wl.layers]})
+    torch.cuda.synchronize()
+    srcs = [wl.source(l) for l in range(len(layers))]
+
+    def step(i, sp=sptr):
+        b = sets[i % n_sets]
+        for l, (_, run, _) in enumerate(layers):
+            kind, k = srcs[l]
+            src = b["in"][k] if kind == "input" else b["out"][k]
+            run(src.data_ptr(), b["out"][l].data_ptr(), M, sp)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # HIP graphs: one per buffer set, each the step's launches, replayed in
+    # the same rotation (the K = 64 path allocates nothing, so it captures).
+    graphs = None
+    if graph and all(L.W.shape[1] == 64 for L in wl.layers):
+        graphs = []
+        for k in range(n_sets):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step(k, torch.cuda.current_stream().cuda_stream)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        # Every replay equals the eager step: eager set 0, replay it twice
+        # with eager work between, compare the last output bit for bit.
+        last = sets[0]["out"][-1]
+        step(0)
+        torch.cuda.synchronize()
+        want = last.clone()
+        for _ in range(2):
+            last.fill_(float("nan"))
+            graphs[0].replay()
+            torch.cuda.synchronize()
+            if not torch.equal(last.view(torch.int32), want.view(torch.int32)):
+                raise RuntimeError("bench.py: a graph replay differs from the eager step")
+            step(1 % n_sets)
+            torch.cuda.synchronize()
+        for i in range(warmup):
+            graphs[i % n_sets].replay()
+        torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for i in range(steps):
+        if graphs is not None:
+            graphs[i % n_sets].replay()
+        else:
+            step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    ms_per_step = ms / steps
+    launches = steps * len(layers)
+    kernel_us = ms * 1e3 / launches
+
+    # Parity of the timed step: the last timed step wrote set (steps - 1) % n_sets.
+    parity = None
+    if args.check:
+        parity = check_timed_step(wl, layers, sets[(steps - 1) % n_sets])
+
+    bytes_step = sum(wl.bytes_per_layer(l) for l in range(len(layers)))
+    ops_step = sum(wl.ops_per_layer(l) for l in range(len(layers)))
+    gbs = bytes_step / (ms_per_step * 1e-3) / 1e9
+    tops = ops_step / (ms_per_step * 1e-3) / 1e12
+    fmt = wl.layers[0].fmt
+    ai = ops_step / bytes_step
+    bound = "hbm" if ai < MFMA_PEAK_TOPS[fmt] * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
+    if name.startswith("c5"):
+        bound = "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
     else:
-        # FP8 (no reference kernel exists): the reference's fake-quant + FP32
-        # Linear composition, restated in the oracle, on one thread.
-        n1 = min(M_all, 4096)
-        t0 = time.perf_counter()
-        O.layer_fp8_composed(wl.x[:n1], L0.W, L0.bias, O.ACT_GELU_TANH)
-        t1 = time.perf_counter() - t0
-        rows_s_1 = rows_s_N = n1 / t1
-        cores = 1
-        kind = "port"
-        sample = (f"FP8 E4M3 fake-quant (fp8_e4m3.h:312-334) + FP32 Linear loop (fno.cpp:68-79), "
-                  f"restated in oracle/, {n1} rows of layer 0 on 1 thread (the reference has "
-                  f"no FP8 GEMM); host {O.host_cpu_model()}")
-    to_unit = wl.samples / total_rows          # samples per row-layer
-    return {
-        "value": rows_s_N * to_unit,
-        "unit": "samples/s",
-        "cores": cores,
-        "kind": kind,
-        "sample": sample,
-        "value_1core": rows_s_1 * to_unit,
-        "layer_rows_per_s": rows_s_N,
-    }
+        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_PEAK_TOPS[fmt],
+                "unit": "TFLOP/s" if fmt == "fp8" else "TOPS",
+                "frac": round(tops / MFMA_PEAK_TOPS[fmt], 4), "traffic": None}
+    kernel = _kernel_of(wl)
+    roof.update({"kernel": kernel,
+                 "kernel_avg_us": round(kernel_us, 3),
+                 "bytes_per_launch": bytes_step // len(layers),
+                 "ops_per_launch": ops_step // len(layers),
+                 "tops": round(tops, 2), "gbs": round(gbs, 1)})
+    if kernel == "nfq::k_gemm_pipe":
+        # The layer is two launches (quantise, then the GEMM); the roofline
+        # is the GEMM kernel's own, timed alone on layer 0's shape.
+        g_us, g_bytes, g_ops = time_gemm_only(wl, layers, sets, stream, max(20, steps))
+        g_gbs, g_tops = g_bytes / (g_us * 1e-6) / 1e9, g_ops / (g_us * 1e-6) / 1e12
+        roof.update({"layer_avg_us": round(kernel_us, 3), "kernel_avg_us": round(g_us, 3),
+                     "bytes_per_launch": g_bytes, "ops_per_launch": g_ops,
+                     "tops": round(g_tops, 2), "gbs": round(g_gbs, 1)})
+        if bound == "hbm":
+            roof.update({"achieved": round(g_gbs, 1), "frac": round(g_gbs / HBM_PEAK_GBS, 4)})
+        else:
+            roof.update({"achieved": round(g_tops, 2), "frac": round(g_tops / MFMA_PEAK_TOPS[fmt], 4)})
+    roof["traffic"] = measured_traffic(kernel, name)
+
+    copy = None
+    if copy_calib:
+        L0 = wl.layers[0]
+        n_out = M * min(L0.W.shape)          # within both the input and the output
+        srcs_c = [s_["in"][0] for s_ in sets]
+        dsts = [s_["out"][0] for s_ in sets]
+        # torch.neg is one elementwise kernel that reads and writes each
+        # float once (a same-dtype copy_ would go to the runtime's blit).
+        for i in range(3):
+            torch.neg(srcs_c[i % n_sets].view(-1)[:n_out], out=dsts[i % n_sets].view(-1)[:n_out])
+        torch.cuda.synchronize()
+        reps = max(20, steps)
+        ev0.record(stream)
+        for i in range(reps):
+            torch.neg(srcs_c[i % n_sets].view(-1)[:n_out], out=dsts[i % n_sets].view(-1)[:n_out])
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / reps
+        cbytes = 8 * n_out
+        copy = {"kernel": "torch.neg (float32 elementwise)", "bytes_per_launch": cbytes,
+                "avg_us": round(us, 3), "gbs": round(cbytes / (us * 1e-6) / 1e9, 1),
+                "frac_of_peak": round(cbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    cpu = None
+    if cpu_legs:
+        try:
+            cpu = cpu_baseline(wl, layers, cpu_legs)
+        except Exception as e:  # reported, not fatal: the GPU figure stands alone
+            cpu = {"error": f"{type(e).__name__}: {e}"}
+
+    rec = {"wl": wl, "n_sets": n_sets, "graphs": graphs is not None, "ms_per_step": ms_per_step,
+           "value": wl.samples / (ms_per_step * 1e-3), "roofline": roof, "parity": parity, "cpu": cpu,
+           "copy": copy, "gen_s": t_gen}
+    del sets, layers
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return rec
 
 
 def ref_runtime_baseline(model, threads_all, b_all=16, b_one=16, reps=3):
@@ -320,6 +555,24 @@ def bench_runtime_model(args, model, oracle_forward, dtype, cpu_b_all, cpu_b_one
     print(json.dumps(out))
 
 
+def _config_entry(name, rec):
+    wl, roof = rec["wl"], rec["roofline"]
+    e = {"workload": wl.name, "rows": wl.M, "layers": len(wl.layers),
+         "ms_per_step": round(rec["ms_per_step"], 5), "samples_per_s": round(rec["value"], 2),
+         "dtype": wl.layers[0].fmt}
+    e.update({k: roof[k] for k in ("bound", "kernel", "kernel_avg_us", "achieved", "unit", "frac", "tops", "gbs",
+                                   "bytes_per_launch", "ops_per_launch", "traffic")})
+    if "layer_avg_us" in roof:
+        e["layer_avg_us"] = roof["layer_avg_us"]
+    e["parity_vs_oracle"] = rec["parity"]
+    if rec["cpu"] is not None:
+        e["cpu_baseline"] = rec["cpu"]
+    return e
+
+
+CONFIGS = ["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch"]
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -334,206 +587,62 @@ def main():
         bench_fno2d_model(args)
         return
 
-    import numpy as np
     import torch
-    from neuroflow_amd import workloads as WL
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    dev = torch.device("cuda:0")
-    wl = WL.WORKLOADS[args.workload]()
-    layers = build_layers(wl, dev)
-    M = wl.M
-    stream = torch.cuda.current_stream()
-    sptr = stream.cuda_stream
-
-    # Buffer sets: input x and one output per layer, rotated across steps.
-    widths = [wl.x.shape[1]] + [L.W.shape[0] for L in wl.layers]
-    set_bytes = sum(4 * M * w for w in widths)
-    n_sets = args.sets or max(2, min(8, -(-1_100_000_000 // set_bytes)))
-    x0 = torch.from_numpy(wl.x).to(dev)
-    sets = []
-    for _ in range(n_sets):
-        bufs = [x0.clone()] + [torch.empty(M, w, dtype=torch.float32, device=dev) for w in widths[1:]]
-        sets.append(bufs)
-    torch.cuda.synchronize()
-
-    def step(i, sp=sptr):
-        bufs = sets[i % n_sets]
-        for l, (_, run, L) in enumerate(layers):
-            src = bufs[l] if wl.chained else bufs[0]
-            run(src.data_ptr(), bufs[l + 1].data_ptr(), M, sp)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # HIP graphs: one per buffer set, each the step's launches, replayed in
-    # the same rotation (the K = 64 path allocates nothing, so it captures).
-    graphs = None
-    if args.graph and all(L.W.shape[1] == 64 for L in wl.layers):
-        graphs = []
-        for k in range(n_sets):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                step(k, torch.cuda.current_stream().cuda_stream)
-            graphs.append(g)
-        torch.cuda.synchronize()
-        # Every replay equals the eager step: eager set 0, replay it twice
-        # with eager work between, compare the last output bit for bit.
-        last = sets[0][-1]
-        step(0)
-        torch.cuda.synchronize()
-        want = last.clone()
-        for _ in range(2):
-            last.fill_(float("nan"))
-            graphs[0].replay()
-            torch.cuda.synchronize()
-            if not torch.equal(last.view(torch.int32), want.view(torch.int32)):
-                raise RuntimeError("bench.py: a graph replay differs from the eager step")
-            step(1 % n_sets)
-            torch.cuda.synchronize()
-        for i in range(args.warmup):
-            graphs[i % n_sets].replay()
-        torch.cuda.synchronize()
-
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for i in range(args.steps):
-        if graphs is not None:
-            graphs[i % n_sets].replay()
-        else:
-            step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1)
-    ms_per_step = ms / args.steps
-    launches = args.steps * len(layers)
-    kernel_us = ms * 1e3 / launches
-
-    # Dominant kernel: the most common layer shape (all layers share one shape
-    # in c1-c3; for c4/c5 the bytes/ops are averaged over the step's launches).
-    bytes_step = sum(wl.bytes_per_layer(l) for l in range(len(layers)))
-    ops_step = sum(wl.ops_per_layer(l) for l in range(len(layers)))
-    gbs = bytes_step / (ms_per_step * 1e-3) / 1e9
-    tops = ops_step / (ms_per_step * 1e-3) / 1e12
-    fmt = wl.layers[0].fmt
-    ai = ops_step / bytes_step
-    bound = "hbm" if ai < MFMA_PEAK_TOPS[fmt] * 1e12 / (HBM_PEAK_GBS * 1e9) else "mfma"
-    if args.workload.startswith("c5"):
-        bound = "mfma"
-    if bound == "hbm":
-        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
-    else:
-        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_PEAK_TOPS[fmt],
-                "unit": "TFLOP/s" if fmt == "fp8" else "TOPS",
-                "frac": round(tops / MFMA_PEAK_TOPS[fmt], 4), "traffic": None}
-    N0, K0 = wl.layers[0].W.shape
-    if K0 == 64 and N0 == 64:
-        kernel = "nfq::k_rows64"
-    elif (wl.layers[0].fmt == "int8" and all(l.W.shape[1] in (128, 256, 512) and l.W.shape[0] % 64 == 0
-                                             for l in wl.layers)):
-        kernel = "nfq::k_token_gemm"    # the whole per-token layer in one launch
-    elif K0 % 64 == 0 and K0 >= 128 and wl.layers[0].fmt == "int8":
-        kernel = "nfq::k_gemm_pipe"     # after a per-token quantise launch
-    else:
-        kernel = "nfq::k_rows"
-    roof.update({"kernel": kernel,
-                 "kernel_avg_us": round(kernel_us, 3),
-                 "bytes_per_launch": bytes_step // len(layers),
-                 "ops_per_launch": ops_step // len(layers),
-                 "tops": round(tops, 2), "gbs": round(gbs, 1)})
-    if kernel == "nfq::k_gemm_pipe":
-        # The layer is two launches (quantise, then the GEMM); the roofline
-        # is the GEMM kernel's own, timed alone on layer 0's shape.
-        g_us, g_bytes, g_ops = time_gemm_only(wl, layers, sets, stream, max(20, args.steps))
-        g_gbs, g_tops = g_bytes / (g_us * 1e-6) / 1e9, g_ops / (g_us * 1e-6) / 1e12
-        roof.update({"layer_avg_us": round(kernel_us, 3), "kernel_avg_us": round(g_us, 3),
-                     "bytes_per_launch": g_bytes, "ops_per_launch": g_ops,
-                     "tops": round(g_tops, 2), "gbs": round(g_gbs, 1)})
-        if bound == "hbm":
-            roof.update({"achieved": round(g_gbs, 1), "frac": round(g_gbs / HBM_PEAK_GBS, 4)})
-        else:
-            roof.update({"achieved": round(g_tops, 2), "frac": round(g_tops / MFMA_PEAK_TOPS[fmt], 4)})
-    roof["traffic"] = measured_traffic(kernel, args.workload)
-
-    parity = None
-    if args.check:
-        from oracle import oracle as O
-        # Re-run layer 0 on the first rows and compare with the oracle.
-        n = min(M, 512)
-        L0 = wl.layers[0]
-        obj = layers[0][0]
-        y = obj(torch.from_numpy(wl.x[:n]).to(dev), L0.act).cpu().numpy()
-        act = {"none": 0, "relu": 1, "gelu": 2}[L0.act]
-        if L0.fmt == "int8":
-            ref, _ = O.layer_per_token_i8(wl.x[:n], obj.W_q, obj.scale_W, None, L0.bias, obj.sum_W, act)
-        else:
-            qa, sa = O.quantise_per_token_fp8(wl.x[:n])
-            ref = O.layer_fp8_exact(qa, sa, obj.W_q, obj.scale_W, L0.bias, act)
-        parity = bool(np.allclose(y, ref, rtol=1e-5, atol=1e-6))
-
-    copy = None
-    if args.copy_calib:
-        L0 = wl.layers[0]
-        n_out = M * min(L0.W.shape)          # within both the input and the output
-        srcs = [s_[0] for s_ in sets]
-        dsts = [s_[1] for s_ in sets]
-        # torch.neg is one elementwise kernel that reads and writes each
-        # float once (a same-dtype copy_ would go to the runtime's blit).
-        for i in range(3):
-            torch.neg(srcs[i % n_sets].view(-1)[:n_out], out=dsts[i % n_sets].view(-1)[:n_out])
-        torch.cuda.synchronize()
-        reps = max(20, args.steps)
-        ev0.record(stream)
-        for i in range(reps):
-            torch.neg(srcs[i % n_sets].view(-1)[:n_out], out=dsts[i % n_sets].view(-1)[:n_out])
-        ev1.record(stream)
-        torch.cuda.synchronize()
-        us = ev0.elapsed_time(ev1) * 1e3 / reps
-        cbytes = 8 * n_out
-        copy = {"kernel": "torch.neg (float32 elementwise)", "bytes_per_launch": cbytes,
-                "avg_us": round(us, 3), "gbs": round(cbytes / (us * 1e-6) / 1e9, 1),
-                "frac_of_peak": round(cbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-
-    cpu = None
+    head = args.workload
+    legs = None
     if not args.no_cpu_baseline:
-        try:
-            cpu = cpu_baseline(wl, layers, args)
-        except Exception as e:  # reported, not fatal: the GPU figure stands alone
-            cpu = {"error": f"{type(e).__name__}: {e}"}
+        legs = ("fp8",) if head == "c3" else ("token", "batched")
+    print(f"bench.py: {head} ({args.steps} steps, {args.warmup} warm-up)", file=sys.stderr, flush=True)
+    rec = bench_workload(head, args, args.steps, args.warmup, cpu_legs=legs, copy_calib=args.copy_calib,
+                         graph=args.graph)
+    wl, roof = rec["wl"], rec["roofline"]
 
-    value = wl.samples / (ms_per_step * 1e-3)
+    configs = {}
+    if not args.no_configs:
+        # Every other workload configuration, measured the same way (fewer
+        # steps), with its parity and a CPU figure of its own.
+        for name in CONFIGS:
+            if name == head:
+                continue
+            print(f"bench.py: {name}", file=sys.stderr, flush=True)
+            c_legs = None if args.no_cpu_baseline else (("fp8",) if name == "c3" else ("token",))
+            r = bench_workload(name, args, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)),
+                               cpu_legs=c_legs)
+            configs[name] = _config_entry(name, r)
+
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(rec["value"], 2),
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(rec["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": fmt,
+        "dtype": wl.layers[0].fmt,
         "data": "synthetic (seeded SplitMix64 inputs, seeded Kaiming-uniform weights)",
         "config": {
             "workload": wl.name,
-            "rows": M,
+            "rows": wl.M,
             "layers": [list(L.W.shape[::-1]) for L in wl.layers],
             "samples_per_step": wl.samples,
-            "buffer_sets": n_sets,
-            "launch": "hip graph per step" if graphs is not None else "stream",
+            "buffer_sets": rec["n_sets"],
+            "launch": "hip graph per step" if rec["graphs"] else "stream",
             "parallelism": "single GPU",
         },
         "roofline": roof,
-        "cpu_baseline": cpu,
-        "parity_vs_oracle": parity,
+        "cpu_baseline": rec["cpu"],
+        "parity_vs_oracle": None if rec["parity"] is None else rec["parity"]["ok"],
+        "parity_detail": rec["parity"],
     }
-    if copy is not None:
-        out["copy_calibration"] = copy
+    if rec["copy"] is not None:
+        out["copy_calibration"] = rec["copy"]
+    if configs:
+        out["configs"] = configs
     print(json.dumps(out))
 
 

@@ -13,7 +13,8 @@ Workloads (rows x K -> N, per layer):
   C1 standalone INT8     32768 x 64 -> 64, N(0,1) activations, GELU
   C2 FNO1d INT8 stack    262144 x 64 -> 64, 4 layers, batch 256 x 1024 points
   C3 FNO2d FP8 stack     1048576 x 64 -> 64, 4 layers, batch 16 x 256 x 256
-  C4 TokenMixer INT8     32768 x 256 -> 768 (qkv) and -> 256 (proj), 6 blocks
+  C4 TokenMixer INT8     32768 x 256 -> 768 (qkv) and -> 256 (proj), 6 blocks, each
+                         layer on its own LayerNorm(N(0,1)) input (attention omitted)
   C5 DeepONet INT8       4096 / 65536 x 1024 -> 1024 (ReLU), trunk head -> 256
 """
 from __future__ import annotations
@@ -90,19 +91,33 @@ class Layer:
     bias: Optional[np.ndarray]    # (N,) fp32
     act: str                      # "gelu" / "relu" / "none"
     fmt: str = "int8"             # "int8" / "fp8"
+    src: Optional[int] = None     # input: inputs[src]; None = the previous layer's output
+                                  # (inputs[0] for the first layer)
 
 
 @dataclass
 class Workload:
     name: str
-    x: np.ndarray                 # (M, K) fp32, the first layer's input
+    x: np.ndarray                 # (M, K) fp32, the first layer's input (inputs[0])
     layers: List[Layer] = field(default_factory=list)
     samples: int = 1              # samples per pass (for samples/s)
-    chained: bool = True          # layer l+1 consumes layer l's output
+    extra: List[np.ndarray] = field(default_factory=list)   # inputs[1:]
 
     @property
     def M(self) -> int:
         return self.x.shape[0]
+
+    @property
+    def inputs(self) -> List[np.ndarray]:
+        return [self.x] + list(self.extra)
+
+    def source(self, l: int):
+        """Where layer l reads its input: ("input", k) for inputs[k], or
+        ("layer", j) for layer j's output."""
+        src = self.layers[l].src
+        if src is not None:
+            return ("input", src)
+        return ("layer", l - 1) if l > 0 else ("input", 0)
 
     def bytes_per_layer(self, l: int) -> int:
         """Algorithmic HBM bytes of one fused layer: 4MK + 4MN + NK*b_w + 8N."""
@@ -152,13 +167,23 @@ def c3_fno2d(batch: int = 16, grid: int = 256, width: int = 64, n_layers: int = 
                     f"width {width}, {n_layers} layers)", x, layers, samples=batch)
 
 
-def c4_tokenmixer(tokens: int = 4096, batch: int = 8, d: int = 256) -> Workload:
+def c4_tokenmixer(tokens: int = 4096, batch: int = 8, d: int = 256, blocks: int = 6) -> Workload:
+    """6 blocks of qkv (d -> 3d) and proj (d -> d), both with bias and no
+    activation.  Each layer reads its own LayerNorm(N(0,1)) input: the
+    attention between qkv and proj and the residual stream are omitted, so
+    block b's qkv reads inputs[2b] and its proj inputs[2b + 1]."""
     M = tokens * batch
-    x = layer_norm(normal(400, (M, d)))
-    qkv = Layer(kaiming_uniform(401, 3 * d, d), uniform(402, (3 * d,), -1 / 16, 1 / 16), "none")
-    proj = Layer(kaiming_uniform(403, d, d), uniform(404, (d,), -1 / 16, 1 / 16), "none")
-    return Workload(f"C4 TokenMixer INT8 block (M={M}, d={d})", x, [qkv, proj], samples=batch,
-                    chained=False)
+    ins, layers = [], []
+    for b in range(blocks):
+        sid = 400 + 10 * b
+        ins.append(layer_norm(normal(sid, (M, d))))
+        ins.append(layer_norm(normal(sid + 5, (M, d))))
+        layers.append(Layer(kaiming_uniform(sid + 1, 3 * d, d), uniform(sid + 2, (3 * d,), -1 / 16, 1 / 16),
+                            "none", src=2 * b))
+        layers.append(Layer(kaiming_uniform(sid + 3, d, d), uniform(sid + 4, (d,), -1 / 16, 1 / 16),
+                            "none", src=2 * b + 1))
+    return Workload(f"C4 TokenMixer INT8 blocks (M={M}, d={d}, {blocks} blocks)", ins[0], layers,
+                    samples=batch, extra=ins[1:])
 
 
 def c5_deeponet_trunk(n_query: int = 65536, width: int = 1024, p: int = 256) -> Workload:

@@ -476,6 +476,8 @@ def ref(variant: str | None = None):
                                                i32, i32, i32]
         L.ref_time_batched_layer.restype = C.c_double
         L.ref_time_batched_layer.argtypes = [C.POINTER(LinearParams), C.c_int64, vp, vp, i32, i32]
+        L.ref_time_fp8_layer.restype = C.c_double
+        L.ref_time_fp8_layer.argtypes = [vp, vp, vp, C.c_int64, i32, i32, vp, i32, i32, i32]
         _ref[variant] = L
     return _ref[variant]
 
@@ -567,6 +569,32 @@ def ref_time_per_token_layer(A, W_q, scale_W, bias, sum_W, threads, reps=3, act_
     t = ref(variant).ref_time_per_token_layer(C.byref(p), A.shape[0], _ptr(A), _ptr(out),
                                               int(act_gelu), threads, reps)
     del keep
+    return t, out
+
+
+def ref_time_batched_layer(A, W_q, scale_W, bias, sum_W, scale_A, threads, reps=3, variant=None):
+    """Median seconds for the reference LinearForwardBatched (one per-tensor
+    scale_A, zp_A = 0) over all rows of A, rows split across threads."""
+    A = _f32(A)
+    N = W_q.shape[0]
+    p, keep = make_params(W_q, scale_W, np.zeros(N, np.int32), bias, scale_A, 0, sum_W)
+    out = np.empty((A.shape[0], N), np.float32)
+    t = ref(variant).ref_time_batched_layer(C.byref(p), A.shape[0], _ptr(A), _ptr(out), threads, reps)
+    del keep
+    return t, out
+
+
+def ref_time_fp8_layer(A, W, bias, threads, reps=3, act_gelu=True, variant=None):
+    """Median seconds for the reference's FP8 composition (per-row
+    fp8_e4m3_per_tensor_fake_quant + the fp32 Linear loop + GELU) over all
+    rows of A, rows split across threads."""
+    A, W = _f32(A), _f32(W)
+    M, K = A.shape
+    N = W.shape[0]
+    b = None if bias is None else _f32(bias)
+    out = np.empty((M, N), np.float32)
+    t = ref(variant).ref_time_fp8_layer(_ptr(A), _ptr(W), _ptr(b), M, K, N, _ptr(out), int(act_gelu),
+                                        threads, reps)
     return t, out
 
 

@@ -185,4 +185,65 @@ double ref_time_batched_layer(const ref_params* p, int64_t M, const float* A, fl
     return times[times.size() / 2];
 }
 
+// Timing of the FP8 composition the reference offers (it has no FP8 GEMM):
+// per row, scale = absmax / 448 and the reference's
+// fp8_e4m3_per_tensor_fake_quant (fp8_e4m3.h:312-334), then the fp32 Linear
+// loop of fno.cpp:68-79 (bias first, products added in k order) against
+// weights fake-quantised once per output channel with the same routine
+// (outside the timed region, as weights are prepared once), then the tanh
+// GELU.  Rows split across threads; median wall time over `reps` passes.
+static void fp8_rows(const float* A, const float* Wq, const float* bias, int K, int N, float* C,
+                     int64_t r0, int64_t r1, int act_gelu) {
+    std::vector<float> xq(K);
+    for (int64_t r = r0; r < r1; ++r) {
+        const float* a = A + r * K;
+        float mx = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const float v = std::fabs(a[k]);
+            if (v > mx) mx = v;
+        }
+        const float s = (mx == 0.0f) ? 1.0f : mx / 448.0f;
+        nflow::fp8_e4m3_per_tensor_fake_quant(a, s, xq.data(), static_cast<size_t>(K));
+        float* y = C + r * N;
+        for (int j = 0; j < N; ++j) {
+            float acc = bias ? bias[j] : 0.0f;
+            const float* w = Wq + static_cast<int64_t>(j) * K;
+            for (int k = 0; k < K; ++k) acc += xq[k] * w[k];
+            y[j] = acc;
+        }
+        if (act_gelu) gelu_row(y, N);
+    }
+}
+
+double ref_time_fp8_layer(const float* A, const float* W, const float* bias, int64_t M, int K, int N,
+                          float* C, int act_gelu, int threads, int reps) {
+    if (threads < 1) threads = 1;
+    std::vector<float> Wq(static_cast<size_t>(N) * K);
+    for (int j = 0; j < N; ++j) {
+        const float* w = W + static_cast<int64_t>(j) * K;
+        float mx = 0.0f;
+        for (int k = 0; k < K; ++k) mx = std::max(mx, std::fabs(w[k]));
+        const float s = (mx == 0.0f) ? 1.0f : mx / 448.0f;
+        nflow::fp8_e4m3_per_tensor_fake_quant(w, s, Wq.data() + static_cast<int64_t>(j) * K,
+                                              static_cast<size_t>(K));
+    }
+    std::vector<double> times;
+    for (int rep = 0; rep < reps; ++rep) {
+        auto t0 = std::chrono::steady_clock::now();
+        std::vector<std::thread> pool;
+        const int64_t chunk = (M + threads - 1) / threads;
+        for (int t = 0; t < threads; ++t) {
+            const int64_t r0 = t * chunk;
+            const int64_t r1 = std::min<int64_t>(M, r0 + chunk);
+            if (r0 >= r1) break;
+            pool.emplace_back(fp8_rows, A, Wq.data(), bias, K, N, C, r0, r1, act_gelu);
+        }
+        for (auto& th : pool) th.join();
+        auto t1 = std::chrono::steady_clock::now();
+        times.push_back(std::chrono::duration<double>(t1 - t0).count());
+    }
+    std::sort(times.begin(), times.end());
+    return times[times.size() / 2];
+}
+
 }  // extern "C"

@@ -37,4 +37,9 @@ def test_small_workload_shapes():
     assert f.x.shape == (128, 64) and len(f.layers) == 4 and f.samples == 2
     t = WL.c4_tokenmixer(tokens=16, batch=2)
     assert t.x.shape == (32, 256) and t.layers[0].W.shape == (768, 256)
-    assert np.allclose(t.x.mean(axis=1), 0, atol=1e-5)
+    assert len(t.layers) == 12 and len(t.inputs) == 12
+    assert [t.source(l) for l in (0, 1, 11)] == [("input", 0), ("input", 1), ("input", 11)]
+    assert not np.array_equal(t.inputs[0], t.inputs[2])
+    for x in t.inputs:
+        assert np.allclose(x.mean(axis=1), 0, atol=1e-5)
+    assert [f.source(l) for l in range(4)] == [("input", 0), ("layer", 0), ("layer", 1), ("layer", 2)]
