@@ -160,6 +160,28 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
                                         const float* A, float* C, float* scale_A_out,
                                         int activation, void* stream);
 
+/* Size of the device scratch behind nflow_int8_linear_forward_per_token_noalloc. */
+#define NFLOW_NOALLOC_SCRATCH_BYTES ((size_t)72 << 20)
+
+/* nflow_int8_linear_forward_per_token that allocates nothing.  No
+ * counterpart in the reference (whose per-token path allocates a
+ * std::vector per call, int8_gemm.cpp:247): it is for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  Same arguments and results, bit for bit.  The
+ * shapes the one-launch kernels do not take (e.g. K = 1024: per-token
+ * quantise into codes, then the tiled GEMM) keep their codes, scales and
+ * byte sums in a static device array of NFLOW_NOALLOC_SCRATCH_BYTES held by
+ * each GPU the library runs on until the process ends, instead of a
+ * stream-ordered allocation.  Workspace = M*K rounded up to 16, + 4M
+ * (scales, unless scale_A_out is given), + 4M (row code sums, with zero
+ * points), + 4N (weight-row sums, with a caller's sum_W); a call needing more
+ * than the array returns NFLOW_INVALID_ARG before anything is launched.
+ * Every call on one GPU shares that array: calls that can overlap on the
+ * device (different streams, not ordered by the caller) race. */
+int nflow_int8_linear_forward_per_token_noalloc(const nflow_int8_linear_params* p, int64_t M,
+                                                const float* A, float* C, float* scale_A_out,
+                                                int activation, void* stream);
+
 /* The FNO local-linear layer (cpp/src/fno.cpp:515-557, 650-654):
  * y = act(x1 + x2) with x2 = the per-token layer above (bias included) and
  * x1 (M, out_features) the spectral branch, in the operation order of the

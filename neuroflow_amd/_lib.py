@@ -85,6 +85,7 @@ SIGNATURES = {
     "nflow_int8_linear_forward_batched": [_P8, _i64, _vp, _vp, _vp],
     "nflow_int8_quantise_per_token": [_vp, _i64, _i32, _vp, _vp, _vp, _vp],
     "nflow_int8_linear_forward_per_token": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
+    "nflow_int8_linear_forward_per_token_noalloc": [_P8, _i64, _vp, _vp, _vp, _i32, _vp],
     "nflow_int8_fno_layer_per_token": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
     "nflow_int8_fno_layer_per_token_x2q": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, C.POINTER(X2QuantC), _vp],
     "nflow_int8_gemm_i32": [_vp, _vp, _i64, _i32, _i32, _vp, _vp],

@@ -599,9 +599,48 @@ static int apply_x2q(RowsArgs& a, const nflow_x2_quant* xq, const char* what) {
     return set_error(NFLOW_INVALID_ARG, w + ": unknown x2 fake-quant kind");
 }
 
+// Device scratch of nflow_int8_linear_forward_per_token_noalloc: the split
+// path's codes, scales and byte sums (at most kNoAllocScratchBytes).  Each
+// GPU the library runs on holds its own copy until the process ends; the
+// name is a host-side stand-in, so host code uses only the device address
+// hipGetSymbolAddress returns for the current device.  Nothing in it needs
+// to start at zero: the quantise launch writes every byte the product reads.
+constexpr size_t kNoAllocScratchBytes = NFLOW_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// The current device's address of `scratch`, looked up on the first call
+// that needs it on that device and kept per device.
+static int noalloc_scratch_address(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    const hipError_t ed = hipGetDevice(&dev);
+    if (ed != hipSuccess) return set_error(NFLOW_INTERNAL, std::string("noalloc scratch: hipGetDevice: ") + hipGetErrorString(ed));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(NFLOW_INTERNAL, "noalloc scratch: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return set_error(NFLOW_INTERNAL, std::string("noalloc scratch: hipGetSymbolAddress: ") + hipGetErrorString(e));
+        addr[dev] = ptr;
+    }
+    *out = addr[dev];
+    return NFLOW_OK;
+}
+
+// The no-allocation entry point's workspace: the library's static device
+// scratch of `cap` bytes, its address looked up (once per device) only after
+// the shape has been checked against `cap`.  Null: allocate on the stream.
+struct FixedWs {
+    size_t cap;
+    const char* what;
+};
+
 static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const float* A,
                           const float* R, float* C, float* scale_A_out, int activation,
-                          const nflow_x2_quant* xq, void* stream) {
+                          const nflow_x2_quant* xq, void* stream, const FixedWs* fixed = nullptr) {
     if (!A || !C || !p || !p->W_int8 || !p->scale_W)
         return set_error(NFLOW_INVALID_ARG, "linear_forward_per_token: null input/output");
     if (p->in_features <= 0 || p->out_features <= 0)
@@ -659,10 +698,37 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
     const bool want_sums = wide && a.zpW;
     const bool want_colsum = wide && a.formula == F_ROW_VNNI && a.sumW;
     const size_t n_sums = (want_sums ? static_cast<size_t>(M) : 0) + (want_colsum ? a.N : 0);
+    const size_t codes16 = ((codes + 15) / 16) * 16;
+    if (fixed) {
+        // Codes, then (with no scale_A_out) M scales, then the sums; every
+        // region is written by the quantise launch before the product reads it.
+        const size_t need = codes16 + (scale_A_out ? 0 : static_cast<size_t>(M) * sizeof(float)) +
+                            n_sums * sizeof(int32_t);
+        if (need > fixed->cap)
+            return set_error(NFLOW_INVALID_ARG, std::string(fixed->what) + ": this shape needs " +
+                                                    std::to_string(need) + " bytes of scratch, more than the " +
+                                                    std::to_string(fixed->cap) + " the library holds (split the rows)");
+        void* base = nullptr;
+        if (int rc = noalloc_scratch_address(&base)) return rc;
+        uint8_t* q = static_cast<uint8_t*>(base);
+        float* sc = scale_A_out ? scale_A_out : reinterpret_cast<float*>(q + codes16);
+        int32_t* sums0 = reinterpret_cast<int32_t*>(q + codes16 + (scale_A_out ? 0 : static_cast<size_t>(M) * sizeof(float)));
+        int32_t* sums = want_sums ? sums0 : nullptr;
+        int32_t* colsum = want_colsum ? sums0 + (want_sums ? M : 0) : nullptr;
+        launch_quantise_token<false>(A, M, a.K, q, sc, sums, st, CodeSums{a.W, a.N, a.K, colsum});
+        a.Aq = q;
+        a.scale_in = sc;
+        a.sum_in = sums;
+        a.colsum_in = colsum;
+        if (wide) launch_gemm<OUT_EPI>(a, act_x2, st);
+        else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, act_x2, st);
+        else launch_generic<false, OUT_EPI>(a, act_x2, st);
+        return finish();
+    }
     Scratch ws(codes + 16 + static_cast<size_t>(M) * sizeof(float) + n_sums * sizeof(int32_t), st);
     if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_per_token: workspace allocation failed");
     uint8_t* q = static_cast<uint8_t*>(ws.p);
-    float* sc = reinterpret_cast<float*>(q + ((codes + 15) / 16) * 16);
+    float* sc = reinterpret_cast<float*>(q + codes16);
     int32_t* sums = want_sums ? reinterpret_cast<int32_t*>(sc + M) : nullptr;
     int32_t* colsum = want_colsum ? reinterpret_cast<int32_t*>(sc + M) + (want_sums ? M : 0) : nullptr;
     launch_quantise_token<false>(A, M, a.K, q, sc, sums, st, CodeSums{a.W, a.N, a.K, colsum});
@@ -686,6 +752,14 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
                                         int activation, void* stream) {
     clear_error();
     return int8_per_token(p, M, A, nullptr, C, scale_A_out, activation, nullptr, stream);
+}
+
+int nflow_int8_linear_forward_per_token_noalloc(const nflow_int8_linear_params* p, int64_t M,
+                                                const float* A, float* C, float* scale_A_out,
+                                                int activation, void* stream) {
+    clear_error();
+    FixedWs fixed{kNoAllocScratchBytes, "linear_forward_per_token_noalloc"};
+    return int8_per_token(p, M, A, nullptr, C, scale_A_out, activation, nullptr, stream, &fixed);
 }
 
 int nflow_int8_fno_layer_per_token(const nflow_int8_linear_params* p, int64_t M, const float* h,

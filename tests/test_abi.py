@@ -97,3 +97,27 @@ def test_layer_handles_reject_bad_arguments():
     assert L.nflow_layer_forward(None, 10, None, None, None, 0, None) == _lib.INVALID_ARG
     assert L.nflow_layer_shape(None, None, None, None) == _lib.INVALID_ARG
     assert L.nflow_layer_destroy(None) == _lib.OK
+
+
+def test_noalloc_rejects_a_workspace_beyond_its_scratch_on_the_host():
+    """nflow_int8_linear_forward_per_token_noalloc checks the split path's
+    workspace (codes + scales + sums) against its static scratch before any
+    device call: a shape that needs more returns InvalidArg with the sizes.
+    (Dummy, never dereferenced pointers: nothing reaches the device.)"""
+    import ctypes as C
+    L = _lib.lib()
+    cap = 72 << 20
+    K = N = 1024
+    M = cap // K + 1                        # the codes alone exceed the scratch
+    dummy = 1 << 20                         # 16-byte aligned, never dereferenced
+    p = _lib.Int8LinearParamsC(C.c_void_p(dummy), C.c_void_p(dummy), C.c_void_p(dummy), None, K, N, 1.0, 0, None)
+    rc = L.nflow_int8_linear_forward_per_token_noalloc(C.byref(p), M, dummy, dummy, None, 1, None)
+    assert rc == _lib.INVALID_ARG
+    msg = L.nflow_last_error().decode()
+    assert "noalloc" in msg and str(cap) in msg and "scratch" in msg
+    # The scales count too when scale_A_out is not given: M * K just under
+    # the cap, plus 4M scales and 4M row sums (zero points), is over it.
+    M2 = (cap - 16) // (K + 8) + 1
+    assert M2 * K <= cap - 16
+    rc = L.nflow_int8_linear_forward_per_token_noalloc(C.byref(p), M2, dummy, dummy, None, 1, None)
+    assert rc == _lib.INVALID_ARG
