@@ -89,6 +89,8 @@ void launch_rows(const RowsArgs& a, int act, hipStream_t st);
 bool rows64_ok(const RowsArgs& a);
 template <bool FP8>
 void launch_rows64(const RowsArgs& a, int act, hipStream_t st);
+// Its fixed-scale INT8 form (one scale_A / zp_A for every row, no activation).
+void launch_rows64_fixed(const RowsArgs& a, hipStream_t st);
 
 // The one-pass per-token INT8 layer for K = 128 / 256 / 512, N % 64 == 0
 // (token_gemm.hip): quantise into LDS, then the whole N range.

@@ -450,6 +450,10 @@ static int int8_fixed_path(const nflow_int8_linear_params* p, int64_t rows, cons
     a.formula = formula;
     a.kb_dot = kb_dot_for(formula, a.K);
     a.C = C;
+    if (rows64_ok(a) && !path_flag(kernel_path().no_rows64)) {
+        launch_rows64_fixed(a, st);
+        return check_launch(what);
+    }
     if (rows_ok(a, IN_F32_FIXED)) {
         launch_rows<false, IN_F32_FIXED, OUT_EPI>(a, ACT_NONE, st);
         return check_launch(what);

@@ -14,9 +14,9 @@ bool rows64_ok(const RowsArgs& a) {
 #define NFQ_ROWS64_PF 1
 #endif
 
-template <bool FP8, int ACT, bool RES, int XQ>
+template <bool FP8, int ACT, bool RES, int XQ, bool FIXED = false>
 static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
-    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES, XQ>;
+    auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES, XQ, FIXED>;
     static const int per_cu = resident_blocks(kern);
     // Persistent waves that all take the same number of tiles (to within
     // one): the fewest waves that keep the per-wave count of a full grid.
@@ -53,6 +53,12 @@ void launch_rows64(const RowsArgs& a, int act, hipStream_t st) {
     if (a.xq_kind == 1) launch_rows64_xq<FP8, 1>(a, act, st);
     else if (a.xq_kind == 2) launch_rows64_xq<FP8, 2>(a, act, st);
     else launch_rows64_xq<FP8, 0>(a, act, st);
+}
+
+// The fixed-scale INT8 layer (LinearForwardBatched / LinearForward rows at
+// K = N = 64): no activation, a.scale_A / a.zp_A for every row.
+void launch_rows64_fixed(const RowsArgs& a, hipStream_t st) {
+    launch_rows64_act<false, ACT_NONE, false, 0, true>(a, st);
 }
 
 template void launch_rows64<false>(const RowsArgs&, int, hipStream_t);

@@ -110,6 +110,32 @@ __device__ __forceinline__ int32_t quant_i8_near(float a, float inv_s, uint64_t&
     return static_cast<int32_t>(r);
 }
 
+// Fixed-scale INT8 code (QuantiseActivation with scale_A, zp_A) by the
+// reciprocal, and whether it is certainly the reference's.  inv = fl(1 / s)
+// correctly rounded and, for s in [2^-120, 2^120] (the caller's condition),
+// normal; t = fl(a * inv) and q = fl(a / s) then each lie within
+// 2^-24 |a / s| (t: 2 * 2^-24) of a / s, so |t - q| <= 3 * 2^-24 |a / s|
+// < 2^-22 |t| (a subnormal product is below 2^-126 and gives r = q = 0).
+// |t - r| with r = rint(t) is exact (t and r within a factor 2, or r = 0).
+// If |t - r| < 0.5 - 2^-20 |t| (so |t| < 2^19), then |q - r| < 0.5:
+// round-half-away(q) == r, and the code is clamp(r + zp) with the
+// reference's wrapping add.  NaN / Inf elements give a NaN distance and are
+// rejected.
+__device__ __forceinline__ int32_t quant_i8_fixed_near(float a, float inv, int32_t zp, bool& bad) {
+    const float t = a * inv;
+    const float r = rintf(t);
+    const float lim = __builtin_fmaf(fabsf(t), -0x1p-20f, 0.5f);
+    bad = !(fabsf(t - r) < lim);
+    const int32_t ri = bad ? 0 : static_cast<int32_t>(r);
+    return clamp_i8(static_cast<int32_t>(static_cast<uint32_t>(ri) + static_cast<uint32_t>(zp)));
+}
+
+// The exact code of element e of x (kept out of line: the rare patch path).
+__device__ __attribute__((noinline)) uint32_t patch_fixed_code(uint32_t word, float v, int e, float s, int32_t zp) {
+    const uint32_t c = static_cast<uint32_t>(quant_i8_exact(v, s, zp)) & 0xFFu;
+    return (word & ~(0xFFu << (8 * e))) | (c << (8 * e));
+}
+
 // A row takes the exact path when its fast absmax is NaN (a signalling NaN
 // in the row) or, for INT8, when amax / 127 would be subnormal (t may then
 // leave the int8 range).
@@ -131,8 +157,13 @@ __device__ __attribute__((noinline)) uint32_t pack4_token_scale(v4f v, float s) 
 // XQ: the x2 fake-quant before it (fno.cpp:572-648): 1 per-tensor
 // (a.xq_scale, a.xq_zpf), 2 per-position (index column * a.xq_points +
 // row % a.xq_points into a.xq_scales / a.xq_zps).
-template <bool FP8, int ACT, int PF = 1, bool RES = false, int XQ = 0>
+// FIXED (INT8 only): one per-tensor scale a.scale_A and zero point a.zp_A
+// for every row (QuantiseActivation, int8_gemm.cpp:507-520, as
+// LinearForwardBatched and LinearForward run it) instead of the per-row
+// absmax; the epilogue's integer formula is a.formula's.
+template <bool FP8, int ACT, int PF = 1, bool RES = false, int XQ = 0, bool FIXED = false>
 __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
+    static_assert(!(FIXED && FP8), "the fixed-scale mode is INT8");
     constexpr bool INT_EPI = !FP8;
     using L = Rows64Lds<FP8>;
     const int lane = threadIdx.x & 63;
@@ -208,6 +239,11 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         }
     }
     const bool all_triv = triv[0] & triv[1] & triv[2] & triv[3];
+    // FIXED: the correctly rounded reciprocal of the scale, and whether the
+    // scale is outside the range where the reciprocal codes are certain (then
+    // every element takes the exact quotient).
+    const float fixed_inv = FIXED ? 1.0f / a.scale_A : 0.0f;
+    const bool fixed_exact = FIXED && !(a.scale_A >= 0x1p-120f && a.scale_A <= 0x1p120f);
     __syncthreads();
 
     for (; tile < ntiles; tile += nwaves) {
@@ -232,6 +268,34 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
                 res[nt] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rr, (r * 64 + 16 * nt + 4 * g) * 4, 0, kCpolNt));
         }
 
+        const int lc = lane & 15;
+        uint32_t q[FP8 ? 8 : 4];
+        uint64_t slow = 0;
+        float s_r;
+        if constexpr (FIXED) {
+            // One scale for all rows; the rare elements the reciprocal cannot
+            // settle are patched with the exact quotient one by one.
+            s_r = a.scale_A;
+            uint32_t badm = 0;   // bit 4j + e: element e of x[j]
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                int32_t c[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bool bad;
+                    c[e] = quant_i8_fixed_near(x[j][e], fixed_inv, a.zp_A, bad);
+                    badm |= (bad || fixed_exact) ? (1u << (4 * j + e)) : 0u;
+                }
+                q[j] = pack4(c[0], c[1], c[2], c[3]);
+            }
+            if (__builtin_amdgcn_ballot_w64(badm != 0)) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (badm & (1u << (4 * j + e))) q[j] = patch_fixed_code(q[j], x[j][e], e, s_r, a.zp_A);
+            }
+        } else {
         // Row absmax in the linear layout: amax[j] = absmax of row 4j + lr.
         float amax[4];
 #pragma unroll
@@ -245,9 +309,9 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             const float v = bperm_f((r & 3) * 16, amax[j]);
             am_r = ((r >> 2) == j) ? v : am_r;
         }
-        uint64_t slow = __builtin_amdgcn_ballot_w64(amax_needs_exact<FP8>(am_r));
+        slow = __builtin_amdgcn_ballot_w64(amax_needs_exact<FP8>(am_r));
         const float qmax = FP8 ? 448.0f : 127.0f;
-        float s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
+        s_r = (am_r == 0.0f) ? 1.0f : am_r / qmax;
         // FP8 scales down by the correctly rounded 1 / s, as the reference.
         float inv_r = FP8 ? ((s_r == 0.0f) ? 1.0f : 1.0f / s_r) : __builtin_amdgcn_rcpf(s_r);
 
@@ -257,8 +321,6 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         for (int j = 0; j < 4; ++j) inv[j] = bperm_f(4 * j + lr, inv_r);
 
         // Quantise in the linear layout.
-        const int lc = lane & 15;
-        uint32_t q[FP8 ? 8 : 4];
         if constexpr (FP8) {
             // Fast path: no NaN among x * inv (a NaN sets the mask; the
             // reference's NaN byte makes the whole output row NaN).
@@ -318,7 +380,8 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
                 for (int j = 0; j < 4; ++j) q[j] = pack4_token_scale(x[j], bperm_f(4 * j + lr, s_r));
             }
         }
-        if (a.scale_out) {
+        }  // per-row scales
+        if (!FIXED && a.scale_out) {
             // Every lane of row r stores the same value; rows >= M are dropped.
             const auto rs = tile_rsrc(a.scale_out, tile * 16, M, 4);
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_r), rs, r * 4, 0, 0);

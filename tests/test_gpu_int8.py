@@ -2,6 +2,7 @@
 accumulators and dequantised outputs; GELU within 1e-5 rel / 1e-6 abs)."""
 import contextlib
 import ctypes
+import functools
 
 import numpy as np
 import pytest
@@ -145,6 +146,53 @@ def test_linear_forward_matches_reference_formulas(gpu, M, N, K, zp_a, with_sum)
     rc, ref_b = O.linear_forward_batched(A, q, s, zps, b, 0.02, zp_a, sumW)
     assert rc == 0
     assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(A))), ref_b)
+
+
+# The fixed-scale K = N = 64 kernel (k_rows64 FIXED, what LinearForwardBatched
+# and LinearForward run at the FNO local-linear shape): sizes with one tile per
+# wave (1000), several (262144) and the doubled grid with a partial last tile
+# (1048581); scales in the reciprocal fast path, at powers of two (exact ties
+# k + 0.5), zero (every quotient inf / NaN), below and above its range.
+FIXED_SCALES = [(0.02, 0), (0.02, 5), (0.25, -3), (0.0, 0), (1e-38, 2), (3e36, 4), (1e30, 3)]
+
+
+@functools.lru_cache(maxsize=4)
+def _fixed_input(M):
+    return WL.normal(70, (M, 64)) * 3.0
+
+
+@pytest.mark.parametrize("M", [1, 1000, 262144, 1048581])
+@pytest.mark.parametrize("scale,zp_a", FIXED_SCALES)
+@pytest.mark.parametrize("form", ["batched", "rows"])
+def test_fixed_scale_k64_kernel(gpu, M, scale, zp_a, form):
+    N = K = 64
+    A = _fixed_input(M).copy()
+    if M >= 16:
+        A[1, :] = (np.arange(K, dtype=np.float32) - 32.0 + 0.5) * 0.25    # ties when scale = 0.25
+        A[2, :8] = [np.nan, np.inf, -np.inf, 3e9, -3e9, 1e-40, -0.0, 1e38]
+        A[3, :] = 0.0
+        A[M // 2, :] = (np.arange(K, dtype=np.float32) + 0.5) * 0.02      # near-ties at 0.02
+    _, q, s, zps, sw, b = _weights(N, K, 71, zp=True)
+    sumW = sw if form == "batched" else None
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), scale_A=scale, zp_A=zp_a,
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    x = _cu(A)
+    run = Q.linear_forward_batched if form == "batched" else Q.linear_forward
+    got = _host(run(p, x))
+    rows = np.arange(M) if M <= 4096 else np.unique(np.concatenate(
+        [np.arange(1024), np.arange(M - 4096, M), np.arange(0, M, 61), [M // 2]]))
+    oracle = O.linear_forward_batched if form == "batched" else O.linear_forward_rows
+    rc, want = oracle(A[rows], q, s, zps, b, scale, zp_a, sumW)
+    assert rc == 0
+    fin = ~np.isnan(want)
+    assert np.array_equal(np.isnan(got[rows]), ~fin)
+    assert _bits_equal(got[rows][fin], want[fin])
+    if M <= 262144:
+        with _env(NFLOW_NO_ROWS64="1"):
+            generic = _host(run(p, x))
+        keep = ~np.isnan(generic)
+        assert np.array_equal(np.isnan(got), ~keep)
+        assert _bits_equal(got[keep], generic[keep])
 
 
 def test_quantised_entry_matches_fused(gpu):
