@@ -196,3 +196,125 @@ def write_binary(op_code: int, config: List[int], activation: str, weights: Dict
             else:
                 raise ValueError(f"unknown qparam kind {kind}")
     return b"".join(out)
+
+
+# ---- symmetric qparams: the exporter side of the device path -----------------
+#
+# The reference's calibration writes asymmetric qparams (min/max ranges,
+# neuroflow/quant/static_quant.py:480-589), and its INT8 GEMM folds nonzero
+# zero points in with formulas that differ between entry points
+# (cpp/src/int8_gemm.cpp:386-393, 461-466, 573-575).  The functions below
+# write symmetric ones instead -- zero point 0, scale = absmax / 127 (INT8)
+# or absmax / 448 (FP8 E4M3) -- in the reference's own qparam dict shape
+# (neuroflow/quant/static_quant.py:1120-1139) and NIRQ layout
+# (neuroflow/ir/export.py:570-643), so an IR drives EnableInt8Gemm /
+# LinearDispatchTryInt8 and the device layers with exact integer products.
+# A zero range gives scale 1 with zero point 0, the reference's choice for a
+# constant tensor (static_quant.py:508-514).
+
+INT8_QMAX = 127.0
+FP8_QMAX = 448.0
+
+
+def _absmax(x) -> np.float32:
+    a = np.asarray(x, np.float32)
+    if a.ndim == 0:
+        return np.float32(abs(float(a)))
+    return np.float32(np.max(np.abs(a))) if a.size else np.float32(0.0)
+
+
+def _scale(absmax, qmax: float) -> np.ndarray:
+    """fl(absmax / qmax) in float32 (1 where absmax is 0 or not finite)."""
+    am = np.asarray(absmax, np.float32)
+    ok = np.isfinite(am) & (am > 0)
+    return np.where(ok, am / np.float32(qmax), np.float32(1.0)).astype(np.float32)
+
+
+def symmetric_per_channel(W: np.ndarray, channel_axis: int = 0) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-channel symmetric INT8 weight qparams: scales[c] = absmax of slice c
+    along `channel_axis` / 127 (float32), zero points 0."""
+    w = np.moveaxis(np.asarray(W, np.float32), channel_axis, 0)
+    am = np.max(np.abs(w.reshape(w.shape[0], -1)), axis=1) if w.size else np.zeros(w.shape[0], np.float32)
+    return _scale(am, INT8_QMAX), np.zeros(w.shape[0], np.int32)
+
+
+def symmetric_per_tensor(x) -> Tuple[float, int]:
+    """Per-tensor symmetric INT8 activation qparam from a calibration tensor
+    (or its absmax): (absmax / 127, 0)."""
+    return float(_scale(_absmax(x), INT8_QMAX)), 0
+
+
+def symmetric_per_token(absmax_per_token, width: int) -> Tuple[np.ndarray, np.ndarray, int]:
+    """Static per-token symmetric INT8 qparams (one scale per token position,
+    NIRQ kind 2): (absmax[t] / 127, zeros, width)."""
+    am = np.asarray(absmax_per_token, np.float32).reshape(-1)
+    return _scale(am, INT8_QMAX), np.zeros(am.size, np.int32), int(width)
+
+
+def fp8_per_tensor(x) -> float:
+    """Per-tensor FP8 E4M3 activation scale: absmax / 448."""
+    return float(_scale(_absmax(x), FP8_QMAX))
+
+
+def symmetric_quant(weights: Dict[str, np.ndarray], weight_names: List[str],
+                    activations: Optional[Dict[str, object]] = None,
+                    per_token: Optional[Dict[str, Tuple[np.ndarray, int]]] = None,
+                    fp8_activations: Optional[Dict[str, object]] = None) -> dict:
+    """The `quant` dict of neuroflow/quant/static_quant.py:1120-1139
+    ({"enabled": True, "qparams": {name: entry}}) with symmetric entries:
+    per-channel (axis 0) for each name in weight_names, per-tensor INT8 for
+    each activation (a calibration tensor or its absmax), static per-token
+    INT8 for each (absmax per token, width) in per_token, FP8 E4M3 for each
+    fp8 activation."""
+    qp: Dict[str, dict] = {}
+    for name in weight_names:
+        s, z = symmetric_per_channel(weights[name], 0)
+        qp[name] = {"per_channel": True, "channel_axis": 0, "scales": s, "zero_points": z}
+    for name, x in (activations or {}).items():
+        s, z = symmetric_per_tensor(x)
+        qp[name] = {"scale": s, "zero_point": z}
+    for name, (am, width) in (per_token or {}).items():
+        s, z, w = symmetric_per_token(am, width)
+        qp[name] = {"per_token": True, "scales": s, "zero_points": z, "width": w}
+    for name, x in (fp8_activations or {}).items():
+        qp[name] = {"format": "fp8_e4m3", "scale": fp8_per_tensor(x)}
+    return {"enabled": True, "qparams": qp}
+
+
+def _qparam_tuples(quant: dict) -> List[tuple]:
+    """The records of a `quant` dict in write_binary's form, in the dict's
+    order, choosing the kind as neuroflow/ir/export.py:612-643 does
+    (per_token, then per_channel, then the FP8 format, else per tensor)."""
+    out = []
+    for name, q in quant.get("qparams", {}).items():
+        if q.get("per_token", False):
+            out.append((2, name, q["scales"], q["zero_points"], int(q.get("width", 0))))
+        elif q.get("per_channel", False):
+            out.append((1, name, q["scales"], q["zero_points"], int(q.get("channel_axis", 0))))
+        elif q.get("format") == "fp8_e4m3":
+            out.append((3, name, float(q["scale"])))
+        else:
+            out.append((0, name, float(q["scale"]), int(q["zero_point"])))
+    return out
+
+
+def export_symmetric(data: bytes, activations: Optional[Dict[str, object]] = None,
+                     per_token: Optional[Dict[str, Tuple[np.ndarray, int]]] = None,
+                     fp8_activations: Optional[Dict[str, object]] = None,
+                     weight_names: Optional[List[str]] = None) -> bytes:
+    """A NeuroIR binary whose NIRQ block holds symmetric qparams: the file's
+    header and weights unchanged, any earlier NIRQ block replaced.
+    weight_names defaults to every 2-D "*.weight" tensor of the file (the
+    Linear weights EnableInt8Gemm looks up: lift, locs.{i}, proj_q,
+    proj_out for FNO1d, fno.cpp:360-406)."""
+    ir = IR(data=data)
+    try:
+        names = ir.weight_names()
+        weights = {n: ir.weight(n) for n in names}
+        op_code, version, config, act = ir.op_code, ir.version, ir.config, ir.activation
+    finally:
+        ir.close()
+    if weight_names is None:
+        weight_names = [n for n in names if n.endswith(".weight") and weights[n].ndim == 2]
+    quant = symmetric_quant(weights, weight_names, activations, per_token, fp8_activations)
+    return write_binary(op_code, config[:_CFG_LEN[op_code]], act, weights, _qparam_tuples(quant), version)

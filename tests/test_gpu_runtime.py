@@ -186,3 +186,46 @@ def test_fp8_codec_functions(gpu):
     assert np.array_equal(b, O.e4m3_encode(x))
     assert np.array_equal(_bits(ncpp.fp8_e4m3_from_bits(b)), _bits(O.e4m3_decode(b)))
     assert np.array_equal(_bits(ncpp.fp8_e4m3_fake_quant(x[4:], 0.5)), _bits(O.fp8_fake_quant(x[4:], 0.5)))
+
+
+@pytest.mark.parametrize("relu", [False, True])
+def test_exported_symmetric_ir_runs_int8(gpu, tmp_path, relu):
+    """An FNO1d IR given symmetric qparams by neuroflow_amd.ir.export_symmetric
+    (per-channel weights, per-tensor inputs of every local-linear layer)
+    sends every locs.{i} to the INT8 GEMM with zero points 0, and the
+    runtime equals the oracle and the reference runtime bit for bit."""
+    from neuroflow_amd import ir as IRM
+    ncpp = load()
+    b, n, ci, co, w, modes, L = 4, 256, 2, 1, 32, 12, 4
+    rng = np.random.default_rng([w, L, int(relu), 11])
+    weights = F.fno1d_weights(rng, ci, co, w, modes, L)
+    cfg = [ci, co, w, modes, L, 1, 0]
+    plain = F.fno1d_file(weights, cfg, None, act=1 if relu else 0)
+    acts = {"lift.output": 1.5, **{f"locs.{i}.output": 2.0 + i for i in range(L)}}
+    ir = IRM.export_symmetric(plain, activations=acts)
+    x = rng.standard_normal((b, n, ci)).astype(np.float32)
+    names = [k for k, v in weights.items() if v.ndim == 2 and k.endswith(".weight")]
+    recs = IRM._qparam_tuples(IRM.symmetric_quant(weights, names, acts))
+    m = OF.from_records(cfg, relu, weights, recs)
+    OF.enable_int8_gemm(m)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    rt = ncpp.InferenceRuntime(str(path))
+    rt.enable_int8_gemm()
+    h = C.c_void_p()
+    lib = _lib.lib()
+    assert lib.nflow_runtime_create_memory(ir, len(ir), C.byref(h)) == 0
+    try:
+        assert lib.nflow_runtime_enable_int8_gemm(h) == 0
+        for i in range(L):
+            u = C.c_int(-1)
+            assert lib.nflow_runtime_layer_dispatch(h, i, C.byref(u)) == 0
+            assert u.value == 1, i
+    finally:
+        lib.nflow_runtime_destroy(h)
+    y = np.zeros((b, n, co), np.float32)
+    rt.run(x, y)
+    want = OF.forward(m, x)
+    assert np.array_equal(_bits(y), _bits(want)), int((_bits(y) != _bits(want)).sum())
+    if REF_RUN.exists():
+        assert np.array_equal(_bits(y), _bits(ref_run(tmp_path, ir, x, co, True)))

@@ -244,3 +244,87 @@ def test_errors_match_reference(tmp_path, mutate):
     data, _ = _fno1d(quant=False)
     bad = mutate(data)
     assert _our_dump(bad) == _ref_dump(bad, tmp_path)
+
+
+# ---- the symmetric exporter (neuroflow_amd.ir.export_symmetric) -------------
+
+def _sym_scale(a) -> np.float32:
+    """fl32(a / 127) for a float32 a, through a float64 quotient: rounding a
+    double quotient to float32 is the correctly rounded float32 quotient
+    (53 >= 2 * 24 + 2); 1 for a zero range."""
+    a = np.float32(a)
+    return np.float32(1.0) if a == 0 else np.float32(np.float64(a) / 127.0)
+
+
+def _exported(seed=3, n_layers=2, width=8):
+    from neuroflow_amd import ir as IRM
+    rng = np.random.default_rng(seed)
+    w = F.fno1d_weights(rng, 2, 1, width, 3, n_layers)
+    w["locs.0.weight"][2, :] = 0.0                      # a zero channel -> scale 1
+    plain = F.fno1d_file(w, [2, 1, width, 3, n_layers, 1, 0], None)
+    calib = rng.standard_normal((4, 16, width)).astype(np.float32) * 3
+    acts = {"lift.output": calib, "locs.0.output": 2.5, "locs.1.output": 0.0}
+    per_token = {"proj_q.output": (np.abs(rng.standard_normal(16 * width)).astype(np.float32), width)}
+    fp8 = {"proj_out.output": 10.0}
+    out = IRM.export_symmetric(plain, activations=acts, per_token=per_token, fp8_activations=fp8)
+    return out, plain, w, calib, per_token
+
+
+def test_export_symmetric_records_and_closed_form():
+    out, plain, w, calib, per_token = _exported()
+    ir, ir0 = IR(data=out), IR(data=plain)
+    assert (ir.version, ir.op, ir.config, ir.activation) == (ir0.version, ir0.op, ir0.config, ir0.activation)
+    assert ir.quant_enabled and not ir0.quant_enabled
+    assert ir.weight_names() == ir0.weight_names()
+    for n in ir.weight_names():
+        assert np.array_equal(ir.weight(n).view(np.uint32), ir0.weight(n).view(np.uint32))
+    two_d = [n for n, v in w.items() if v.ndim == 2 and n.endswith(".weight")]
+    assert sorted(two_d) == sorted(n for n, k in ir.qparam_records() if k == "per_channel")
+    for n in two_d:
+        s, z, ax = ir.per_channel(n)
+        want = [_sym_scale(np.abs(row).max()) for row in w[n]]
+        assert ax == 0 and np.array_equal(s.view(np.uint32), np.asarray(want, np.float32).view(np.uint32)), n
+        assert not z.any()
+    assert ir.per_channel("locs.0.weight")[0][2] == 1.0
+    assert ir.per_tensor("lift.output") == (_sym_scale(np.abs(calib).max()), 0)
+    assert ir.per_tensor("locs.0.output") == (_sym_scale(2.5), 0)
+    assert ir.per_tensor("locs.1.output") == (1.0, 0)
+    sc, zp, width = ir.per_token("proj_q.output")
+    am, wd = per_token["proj_q.output"]
+    assert width == wd and not zp.any()
+    assert np.array_equal(sc.view(np.uint32), np.asarray([_sym_scale(a) for a in am], np.float32).view(np.uint32))
+    assert ir.fp8("proj_out.output") == np.float32(np.float64(np.float32(10.0)) / 448.0)
+    ir.close()
+    ir0.close()
+
+
+def test_export_symmetric_replaces_an_earlier_block():
+    from neuroflow_amd import ir as IRM
+    data, w = _fno1d(quant=True)
+    out = IRM.export_symmetric(data, activations={"lift.output": 1.0})
+    with IR(data=out) as ir:
+        assert ir.per_tensor("lift.output") == (_sym_scale(1.0), 0)
+        assert ir.per_tensor("locs.0.output") is None and ir.fp8("proj_out.output") is None
+        assert not ir.per_channel("locs.1.weight")[1].any()
+
+
+def test_export_symmetric_codes_reach_127():
+    """QuantiseWeight2D (fno.cpp:340-356, the library's host restatement) on
+    the exported qparams: codes within [-127, 127], +-127 exactly where a
+    channel's absmax is, and the host's per-channel scales agree."""
+    from neuroflow_amd import quant as Q
+    out, _, w, _, _ = _exported(seed=5, width=16)
+    with IR(data=out) as ir:
+        for n in ("lift.weight", "locs.1.weight", "proj_q.weight"):
+            s, z, _ = ir.per_channel(n)
+            q, _ = Q.quantise_weight_2d(w[n], s, z)
+            nz = np.abs(w[n]).max(axis=1) > 0
+            assert np.abs(q).max() <= 127
+            assert np.array_equal(np.abs(q).max(axis=1)[nz], np.full(nz.sum(), 127))
+            assert np.array_equal(Q.per_channel_scales(w[n], 127.0)[nz], s[nz])
+
+
+@needs_ref
+def test_export_symmetric_matches_reference_loader(tmp_path):
+    out, _, _, _, _ = _exported(seed=7, n_layers=3, width=12)
+    assert _our_dump(out) == _ref_dump(out, tmp_path)
