@@ -25,6 +25,8 @@
 //    not being read, two stages.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "rows_kernel.h"
 
@@ -174,6 +176,86 @@ __device__ __forceinline__ void gemm_store(const RowsArgs& a, const v4i (&acc)[T
 
 template <int TN>
 constexpr int gemm_strip_bytes() { return 16 * (16 * TN + 4) * 4; }
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Epilogue of a wave's (TM / 2) x (TN / 2) accumulator tiles of
+// v_mfma_i32_32x32x32_i8 with W as the A operand: value v of lane l in tile
+// (i, j) is row 32 i + l % 32, column 32 j + 8 (v / 4) + 4 (l / 32) + v % 4
+// of the wave's 16 TM x 16 TN tile, so each group of four values is four
+// adjacent columns of one row.  The tile rows go out 16 at a time: the
+// lanes holding them (l % 32 in [16 p, 16 p + 16)) write the strip, the
+// wave reads it back row-contiguously (64 TN bytes per row).
+template <int TM, int TN, int OUT, int ACT>
+__device__ __forceinline__ void gemm_store32(const RowsArgs& a, const v16i (&acc)[TM / 2][TN / 2], int64_t m0,
+                                             int n0, int wm, int wn, uint32_t* strip,
+                                             const float (&srow)[TM / 2], const int32_t (&sa)[TM / 2],
+                                             bool trivial, const IntEpi* lds_e, const float* lds_scw,
+                                             const float* lds_b) {
+    constexpr int I = TM / 2, J = TN / 2;
+    constexpr int SW = 16 * TN + 4;                 // strip row stride (32-bit words)
+    constexpr int CHUNKS = 4 * TN;                  // 16-byte chunks per strip row
+    constexpr int ROWS_PER_INST = 64 / CHUNKS;
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t M = a.M;
+    const int N = a.N;
+    const int ncol0 = n0 + 16 * TN * wn;
+    const int rd_row = lane / CHUNKS, rd_chunk = lane % CHUNKS;
+    const bool col_ok = ncol0 + 4 * rd_chunk < N;
+#pragma unroll
+    for (int i = 0; i < I; ++i) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            if ((r >> 4) == p) {
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int wcol = 32 * j + 8 * q + 4 * h;      // column within the wave tile
+                        const int lcol = 16 * TN * wn + wcol;         // within the block tile
+                        v4u bits;
+                        if constexpr (OUT == OUT_RAW) {
+                            bits = v4u{static_cast<unsigned>(acc[i][j][4 * q]), static_cast<unsigned>(acc[i][j][4 * q + 1]),
+                                       static_cast<unsigned>(acc[i][j][4 * q + 2]), static_cast<unsigned>(acc[i][j][4 * q + 3])};
+                        } else {
+                            const v4f swv = *reinterpret_cast<const v4f*>(lds_scw + lcol);
+                            const v4f bv = *reinterpret_cast<const v4f*>(lds_b + lcol);
+                            v4f y;
+                            if (trivial) {
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    y[v] = activate<ACT>(dequant_bias(swv[v], srow[i], static_cast<float>(acc[i][j][4 * q + v]), bv[v]));
+                            } else {
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    const float t = int_epi_value(lds_e[lcol + v], acc[i][j][4 * q + v], sa[i]);
+                                    y[v] = activate<ACT>(dequant_bias(swv[v], srow[i], t, bv[v]));
+                                }
+                            }
+                            bits = __builtin_bit_cast(v4u, y);
+                        }
+                        *reinterpret_cast<v4u*>(strip + (r & 15) * SW + wcol) = bits;
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int u = 0; u < 16 / ROWS_PER_INST; ++u) {
+                const int srow_i = u * ROWS_PER_INST + rd_row;
+                const v4u v = *reinterpret_cast<const v4u*>(strip + srow_i * SW + 4 * rd_chunk);
+                const int64_t m = m0 + 16 * TM * wm + 32 * i + 16 * p + srow_i;
+                if (m < M && col_ok)
+                    *reinterpret_cast<v4u*>(static_cast<uint32_t*>(a.C) + m * N + ncol0 + 4 * rd_chunk) = v;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+}
 
 // ---------------------------------------------------------------------------
 // k_gemm: register-staged K loop with in-loop byte sums (any zero points).
@@ -344,8 +426,13 @@ __device__ __forceinline__ void gemm_stage_sync() {
 // Row code sums come from a.sum_in and weight-row byte sums from
 // a.colsum_in (null: zero; valid when zpW is null, resp. when the formula
 // does not use them).  zp_A must be 0.
-template <int TM, int TN, int OUT, int ACT>
+//
+// MF selects the MFMA: 16 (v_mfma_i32_16x16x64_i8, TM x TN tiles of 16 x 16
+// per wave) or 32 (v_mfma_i32_32x32x32_i8, (TM / 2) x (TN / 2) tiles of
+// 32 x 32: half the operand reads per product and a higher issue rate).
+template <int TM, int TN, int OUT, int ACT, int MF = 16>
 __global__ __launch_bounds__(256, 2) void k_gemm_pipe(RowsArgs a, int xcd_groups) {
+    static_assert(MF == 16 || (MF == 32 && TM % 2 == 0 && TN % 2 == 0), "32 x 32 tiles need even TM, TN");
     using S = GemmShape<TM, TN>;
     constexpr int BM = S::BM, BN = S::BN;
     constexpr int NL = (BM + BN) / 64;   // 1 KB DMA instructions per wave per K step
@@ -397,12 +484,40 @@ __global__ __launch_bounds__(256, 2) void k_gemm_pipe(RowsArgs a, int xcd_groups
         }
     };
 
-    v4i acc[TM][TN];
+    constexpr int AI = MF == 32 ? TM / 2 : TM, AJ = MF == 32 ? TN / 2 : TN;
+    using Acc = std::conditional_t<MF == 32, v16i, v4i>;
+    Acc acc[AI][AJ];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < AI; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+        for (int j = 0; j < AJ; ++j) acc[i][j] = Acc{};
     auto mma_step = [&](const uint8_t* cur) {
+        if constexpr (MF == 32) {
+            // Lane l reads row l % 32 of each 32-row fragment, 16-byte group
+            // 2 s + l / 32 for K half s: the same k order for both operands.
+            const int r32 = lane & 31, h32 = lane >> 5;
+            v4i xf[2][AI], wf[2][AJ];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+                    xf[s][i] = *reinterpret_cast<const v4i*>(cur + gemm_lds_off(16 * TM * wm + 32 * i + r32, 2 * s + h32));
+#pragma unroll
+                for (int j = 0; j < AJ; ++j)
+                    wf[s][j] = *reinterpret_cast<const v4i*>(cur + BM * GEMM_LDS_ROW +
+                                                             gemm_lds_off(16 * TN * wn + 32 * j + r32, 2 * s + h32));
+            }
+            __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (AI + AJ), 0);  // DS reads
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < AI; ++i)
+#pragma unroll
+                    for (int j = 0; j < AJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[s][j], xf[s][i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0008, 2 * AI * AJ, 0);  // MFMA
+            return;
+        } else {
         v4i xf[TM], wf[TN];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -417,6 +532,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_pipe(RowsArgs a, int xcd_groups
             for (int j = 0; j < TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[j], xf[i], acc[i][j], 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(0x0008, TM * TN, 0);  // MFMA
+        }
     };
 
     // Steps 0 and 1 are loaded before the loop.  Step k (stage k % 3): wait
@@ -450,11 +566,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_pipe(RowsArgs a, int xcd_groups
     // the last step; gemm_epi_tables ends with a barrier).
     static_assert(2 * gemm_strip_bytes<TN>() <= S::STAGE, "two strips fit a stage");
     uint32_t* strip = reinterpret_cast<uint32_t*>((wid < 2 ? st0 : st1) + (wid & 1) * gemm_strip_bytes<TN>());
-    float srow[TM];
-    int32_t sa[TM];
+    // Row of lane l in accumulator row tile i: 16 i + l % 16 (16 x 16) or
+    // 32 i + l % 32 (32 x 32).
+    float srow[AI];
+    int32_t sa[AI];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int64_t m = m0 + 16 * TM * wm + 16 * i + r;
+    for (int i = 0; i < AI; ++i) {
+        const int64_t m = m0 + 16 * TM * wm + (MF == 32 ? 32 * i + (lane & 31) : 16 * i + r);
         srow[i] = 1.0f;
         sa[i] = 0;
         if constexpr (OUT == OUT_EPI) {
@@ -462,7 +580,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_pipe(RowsArgs a, int xcd_groups
             sa[i] = (a.sum_in && m < M) ? a.sum_in[m] : 0;
         }
     }
-    gemm_store<TM, TN, OUT, ACT>(a, acc, m0, n0, wm, wn, strip, srow, sa, trivial, lds_e, lds_scw, lds_b);
+    if constexpr (MF == 32)
+        gemm_store32<TM, TN, OUT, ACT>(a, acc, m0, n0, wm, wn, strip, srow, sa, trivial, lds_e, lds_scw, lds_b);
+    else
+        gemm_store<TM, TN, OUT, ACT>(a, acc, m0, n0, wm, wn, strip, srow, sa, trivial, lds_e, lds_scw, lds_b);
 }
 
 }  // namespace nfq

@@ -44,7 +44,8 @@ inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 // Kernel-selection overrides, for A/B timing and for tests that pin one of
 // two kernels computing the same bits.  They are read from the environment
 // once, at the first launch (NFLOW_NO_GEMM, NFLOW_NO_ROWS64,
-// NFLOW_NO_TOKEN_GEMM, NFLOW_GEMM_REG, NFLOW_GEMM_TILE), and afterwards
+// NFLOW_NO_TOKEN_GEMM, NFLOW_GEMM_REG, NFLOW_GEMM_TILE, NFLOW_GEMM_MFMA,
+// NFLOW_NO_WIDE), and afterwards
 // change only through nflow_debug_set_kernel_path; a launch reads relaxed
 // atomics, never the environment.
 struct KernelPath {
@@ -53,6 +54,8 @@ struct KernelPath {
     std::atomic<int> no_token_gemm{0};
     std::atomic<int> gemm_reg{0};
     std::atomic<int> gemm_tile{0};   // 0: the launcher's choice
+    std::atomic<int> gemm_mfma{0};   // 0: the launcher's choice, else 16 or 32
+    std::atomic<int> no_wide{0};
 };
 KernelPath& kernel_path();
 

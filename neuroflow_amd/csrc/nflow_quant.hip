@@ -403,6 +403,8 @@ KernelPath& kernel_path() {
         p->no_token_gemm.store(env_int("NFLOW_NO_TOKEN_GEMM"));
         p->gemm_reg.store(env_int("NFLOW_GEMM_REG"));
         p->gemm_tile.store(env_int("NFLOW_GEMM_TILE"));
+        p->gemm_mfma.store(env_int("NFLOW_GEMM_MFMA"));
+        p->no_wide.store(env_int("NFLOW_NO_WIDE"));
         return p;
     }();
     return *k;
@@ -500,7 +502,9 @@ int nflow_debug_set_kernel_path(const char* name, int value, int* previous) {
                         : n == "no_rows64" ? &k.no_rows64
                         : n == "no_token_gemm" ? &k.no_token_gemm
                         : n == "gemm_reg" ? &k.gemm_reg
-                        : n == "gemm_tile" ? &k.gemm_tile : nullptr;
+                        : n == "gemm_tile" ? &k.gemm_tile
+                        : n == "gemm_mfma" ? &k.gemm_mfma
+                        : n == "no_wide" ? &k.no_wide : nullptr;
     if (!f) return set_error(NFLOW_INVALID_ARG, "debug_set_kernel_path: unknown name " + n);
     const int old = f->exchange(value, std::memory_order_relaxed);
     if (previous) *previous = old;

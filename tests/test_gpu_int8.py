@@ -352,7 +352,8 @@ def test_gemm_i32_tile_shapes(gpu, M, N, K, tile):
 # The per-token layer's paths: "tiled" forces quantise + tiled GEMM where the
 # one-pass kernel (K = 128 / 256 / 512, N % 64 = 0) would take the shape.
 PATHS = {"auto": {}, "tiled": {"NFLOW_NO_TOKEN_GEMM": "1"}, "tiled22": {"NFLOW_NO_TOKEN_GEMM": "1",
-                                                                       "NFLOW_GEMM_TILE": "22"}}
+                                                                       "NFLOW_GEMM_TILE": "22"},
+         "pipe": {"NFLOW_NO_TOKEN_GEMM": "1", "NFLOW_NO_WIDE": "1"}}
 
 
 @pytest.mark.parametrize("path", list(PATHS))
@@ -456,3 +457,67 @@ def test_token_gemm_layer(gpu, M, N, K, form, act):
     keep = ~np.isnan(split)
     assert np.array_equal(np.isnan(out_all), ~keep)
     assert _bits_equal(out_all[keep], split[keep])
+
+
+# ---- the persistent GEMM (K = 512 / 1024, fused epilogue) --------------------------
+
+# (M, N, K): one partial 128-row tile; N not a multiple of the 128 / 256-column
+# tile; C5's branch (128 x 128 tiles, one per CU); a ragged shape; several
+# 128 x 256 tiles per CU with a partial last row tile; K = 512; C5's trunk
+# (eight 128 x 256 tiles per CU: both accumulator sets, the table parities and
+# the load stream across tile boundaries).
+WIDE_SHAPES = [(1, 1024, 1024), (100, 260, 1024), (4096, 1024, 1024), (10000, 1000, 1024),
+               (20000, 1024, 1024), (3000, 776, 512), (65536, 1024, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", WIDE_SHAPES)
+@pytest.mark.parametrize("form", ["sym", "zp", "zp_sum_off"])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu"])
+def test_wide_gemm_layer(gpu, M, N, K, form, act):
+    """The per-token layer on the persistent GEMM: sampled rows against the
+    oracle (bit-exact without GELU), and every output bit-equal to the
+    LDS-DMA tiled GEMM on the same codes (NFLOW_NO_WIDE), which the tests
+    above pin separately."""
+    A = WL.normal(60, (M, K))
+    if M > 3:
+        A[1] = 0.0
+        A[2, :4] = np.array([np.nan, 1.0, -2.0, 3.0], np.float32)
+    _, q, s, zps, sw, b = _weights(N, K, 61, zp=form != "sym")
+    sumW = sw if form != "zp_sum_off" else (sw + np.arange(N, dtype=np.int32) % 7 - 3).astype(np.int32)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sumW))
+    code = {"none": 0, "relu": 1, "gelu": 2}[act]
+    with _env(NFLOW_NO_TOKEN_GEMM="1"):
+        out = _host(Q.linear_forward_per_token(p, _cu(A), act))
+    with _env(NFLOW_NO_TOKEN_GEMM="1", NFLOW_NO_WIDE="1"):
+        ref_pipe = _host(Q.linear_forward_per_token(p, _cu(A), act))
+    assert _bits_equal(out, ref_pipe)
+    step = max(1, M // 400)
+    rows = np.unique(np.concatenate([np.arange(0, M, step), np.arange(max(0, M - 130), M)]))
+    ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, code)
+    if act == "gelu":
+        np.testing.assert_allclose(out[rows], ref, rtol=RTOL, atol=ATOL)
+    else:
+        finite = np.isfinite(ref)
+        assert _bits_equal(out[rows][finite], ref[finite])
+        assert np.array_equal(np.isnan(out[rows]), np.isnan(ref))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 1024, 1024), (65536, 1024, 1024), (777, 516, 512)])
+@pytest.mark.parametrize("with_sum", [False, True])
+def test_wide_gemm_quantised_codes(gpu, M, N, K, with_sum):
+    """linear_forward_quantised on per-token codes with symmetric weights:
+    without zero points and sum_W the persistent GEMM takes its plain
+    epilogue; with a caller's sum_W the row-VNNI term needs the weight-row
+    byte sums.  Equal to the LDS-DMA tiled GEMM bit for bit, and to the oracle
+    on sampled rows."""
+    A = WL.normal(62, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 63)
+    qa, sa, _ = Q.quantise_per_token(_cu(A))
+    p = Q.Int8LinearParams(_cu(q), _cu(s), None, _cu(b), sum_W_per_row=_cu(sw) if with_sum else None)
+    out = _host(Q.linear_forward_quantised(p, qa, sa, "relu"))
+    with _env(NFLOW_NO_WIDE="1"):
+        ref_pipe = _host(Q.linear_forward_quantised(p, qa, sa, "relu"))
+    assert _bits_equal(out, ref_pipe)
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 300)), [M - 1]]))
+    ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sw if with_sum else None, 1)
+    assert _bits_equal(out[rows], ref)
