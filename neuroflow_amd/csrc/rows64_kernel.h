@@ -59,6 +59,10 @@ __device__ __forceinline__ float row16_absmax_fast(v4f x) {
 
 // Cache-policy operand of the buffer intrinsics: the nt (non-temporal) bit.
 constexpr int kCpolNt = 2;
+// Cache policy of the layer's output stores.
+#ifndef NFQ_ROWS64_STORE_CPOL
+#define NFQ_ROWS64_STORE_CPOL 0
+#endif
 
 __device__ __forceinline__ float bperm_f(int src_lane, float v) {
     return __builtin_bit_cast(float,
@@ -198,43 +202,67 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
 
     int64_t tile = wave;
     v4f pre[PF][4];
-#pragma unroll
-    for (int p = 0; p < PF; ++p) load_lin(tile + p * nwaves, pre[p]);
 
-    if (threadIdx.x < 64) {
-        const int n = threadIdx.x;
-        reinterpret_cast<float*>(lds_sw)[n] = a.sW[n];
-        reinterpret_cast<float*>(lds_b)[n] = a.bias ? a.bias[n] : 0.0f;
-    }
+    // Setup loads first -- the weights, the per-column constants and the
+    // block's scale / bias table -- then the first tile's loads.  Loads
+    // complete in issue order, so the waits for the setup data then do not
+    // include the tile's HBM latency under the launch's initial burst (every
+    // wave requests its first tile at once); with the tile loads first, each
+    // setup wait also waited for the tile, and no tile of a 256 Ki-row layer
+    // completed in its first 6 us (measured).
     // INT8 weights stay in registers: lane (r, g) holds W[16nt + r][16g ..
     // 16g + 15] for nt = 0..3.  FP8 weights go to LDS as bf16 (thread t
     // converts W[t / 4][16 (t % 4) .. + 15]).
     uint32_t wi8[4][4];
-    bool triv[4] = {true, true, true, true};
+    int32_t zpw_c[4] = {0, 0, 0, 0}, sumw_c[4] = {0, 0, 0, 0};   // column 16 nt + r
+    uint32_t w8[4];
     if constexpr (FP8) {
-        const int n = threadIdx.x >> 2, c = threadIdx.x & 3;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + n * 64 + 16 * c);
-        uint32_t b[4], o[8];
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (threadIdx.x >> 2) * 64 + 16 * (threadIdx.x & 3));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b[q] = src[q];
-        bytes_to_bf16_op(b, o);
-        v4u* dst = reinterpret_cast<v4u*>(lds_w + n * W_BF16_STRIDE + 8 * c);
-        dst[0] = v4u{o[0], o[1], o[2], o[3]};
-        dst[1] = v4u{o[4], o[5], o[6], o[7]};
+        for (int q = 0; q < 4; ++q) w8[q] = src[q];
     } else {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (16 * nt + r) * 64 + 16 * g);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wi8[nt][q] = src[q];
+            zpw_c[nt] = a.zpW ? a.zpW[16 * nt + r] : 0;
+            sumw_c[nt] = a.sumW ? a.sumW[16 * nt + r] : 0;
+        }
+    }
+    float sw_n = 0.0f, b_n = 0.0f;
+    if (threadIdx.x < 64) {
+        sw_n = a.sW[threadIdx.x];
+        b_n = a.bias ? a.bias[threadIdx.x] : 0.0f;
+    }
+    asm volatile("" ::: "memory");   // the tile loads stay behind the setup loads
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load_lin(tile + p * nwaves, pre[p]);
+
+    if (threadIdx.x < 64) {
+        reinterpret_cast<float*>(lds_sw)[threadIdx.x] = sw_n;
+        reinterpret_cast<float*>(lds_b)[threadIdx.x] = b_n;
+    }
+    bool triv[4] = {true, true, true, true};
+    if constexpr (FP8) {
+        const int n = threadIdx.x >> 2, c = threadIdx.x & 3;
+        uint32_t o[8];
+        bytes_to_bf16_op(w8, o);
+        v4u* dst = reinterpret_cast<v4u*>(lds_w + n * W_BF16_STRIDE + 8 * c);
+        dst[0] = v4u{o[0], o[1], o[2], o[3]};
+        dst[1] = v4u{o[4], o[5], o[6], o[7]};
+    } else {
+        // The epilogue constants of column 16 nt + r (row_sum4 reduces the
+        // four k-groups' byte sums; K = 64, so the dot covers every k).
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
             int32_t ps = 0;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                wi8[nt][q] = src[q];
-                ps = sum_bytes_i8(wi8[nt][q], ps);
-            }
-            IntEpi mine;
-            ColConsts cc;
-            col_setup<false, OUT_EPI>(a, 16 * nt, r, g, ps, ps, cc, mine, false);
-            triv[nt] = cc.trivial;
+            for (int q = 0; q < 4; ++q) ps = sum_bytes_i8(wi8[nt][q], ps);
+            const int32_t sfull = row_sum4(ps);
+            const IntEpi mine = int_epi_consts(a.formula, a.K, a.zp_A, zpw_c[nt], sumw_c[nt], a.sumW != nullptr,
+                                               sfull, sfull);
+            triv[nt] = !__any((mine.c0 != 0) | (mine.c1 != 0) | (mine.c2 != 0));
             if (wid == 0 && g == 0) lds_e[16 * nt + r] = mine;
         }
     }
@@ -482,7 +510,7 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         const auto rs = tile_rsrc(a.C, tile * 16, M, 256);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, y[j]), rs, lin_off + 1024 * j, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, y[j]), rs, lin_off + 1024 * j, 0, NFQ_ROWS64_STORE_CPOL);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
     }

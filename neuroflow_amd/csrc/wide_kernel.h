@@ -112,6 +112,13 @@ __device__ __forceinline__ void wide_dma(v4u desc, uint32_t lds, int voff, int s
                  : "memory", "m0");
 }
 
+// One dword store of zero to a zero-byte range (dropped by the hardware):
+// asm, so that the compiler cannot merge a run of them into one wider store,
+// which would change the count the waits rely on.
+__device__ __forceinline__ void wide_null_store(v4u desc, int voff) {
+    asm volatile("buffer_store_dword %0, %1, %2, 0 offen" : : "v"(0), "v"(voff), "s"(desc) : "memory");
+}
+
 struct WideTile {
     int64_t m0;
     int n0;
@@ -334,17 +341,19 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     // MFMAs, then slice k of the previous tile's epilogue.  The prologue
     // issues steps 0 and 1, each followed by STORES stores to a zero-byte
     // range: the instruction sequence of a tile's last two steps, so that the
-    // first tile's waits count right.
+    // first tile's waits count right.  (Every wait counts this wave's vector
+    // memory instructions exactly; the drain's stores go to rows N floats
+    // apart, N unknown at compile time, so they cannot be merged either.)
     WideTile cur = wide_tile<BM, BN>(0, ntiles, n_tiles_n);
     if (!cur.valid) return;
     {
-        const auto rs_none = wide_rsrc(nullptr, 0);
+        const v4u none = wide_desc(nullptr, 0);
         dma_step(st_base, cur, 0);
 #pragma unroll
-        for (int q = 0; q < STORES; ++q) __builtin_amdgcn_raw_buffer_store_b32(0u, rs_none, 4 * q, 0, 2);
+        for (int q = 0; q < STORES; ++q) wide_null_store(none, 4 * q);
         dma_step(st_base + Cf::STAGE, cur, 1);
 #pragma unroll
-        for (int q = 0; q < STORES; ++q) __builtin_amdgcn_raw_buffer_store_b32(0u, rs_none, 4 * q, 0, 2);
+        for (int q = 0; q < STORES; ++q) wide_null_store(none, 4 * q);
     }
     WideTile prev{0, 0, false};
     int sc = 0;   // stage of the current step: the global step number mod NS

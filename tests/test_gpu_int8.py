@@ -465,9 +465,12 @@ def test_token_gemm_layer(gpu, M, N, K, form, act):
 # tile; C5's branch (128 x 128 tiles, one per CU); a ragged shape; several
 # 128 x 256 tiles per CU with a partial last row tile; K = 512; C5's trunk
 # (eight 128 x 256 tiles per CU: both accumulator sets, the table parities and
-# the load stream across tile boundaries).
+# the load stream across tile boundaries); 258 tiles of 128 x 128 (most
+# blocks run one tile, whose first steps wait on the prologue's instruction
+# count -- the case where merged prologue stores once broke those waits).
 WIDE_SHAPES = [(1, 1024, 1024), (100, 260, 1024), (4096, 1024, 1024), (10000, 1000, 1024),
-               (20000, 1024, 1024), (3000, 776, 512), (65536, 1024, 1024)]
+               (20000, 1024, 1024), (3000, 776, 512), (65536, 1024, 1024), (33000, 128, 512),
+               (33000, 128, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", WIDE_SHAPES)
@@ -486,11 +489,12 @@ def test_wide_gemm_layer(gpu, M, N, K, form, act):
     sumW = sw if form != "zp_sum_off" else (sw + np.arange(N, dtype=np.int32) % 7 - 3).astype(np.int32)
     p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), sum_W_per_row=_cu(sumW))
     code = {"none": 0, "relu": 1, "gelu": 2}[act]
-    with _env(NFLOW_NO_TOKEN_GEMM="1"):
-        out = _host(Q.linear_forward_per_token(p, _cu(A), act))
     with _env(NFLOW_NO_TOKEN_GEMM="1", NFLOW_NO_WIDE="1"):
         ref_pipe = _host(Q.linear_forward_per_token(p, _cu(A), act))
-    assert _bits_equal(out, ref_pipe)
+    with _env(NFLOW_NO_TOKEN_GEMM="1"):
+        for _ in range(3):   # a missed wait would show as run-to-run differences
+            out = _host(Q.linear_forward_per_token(p, _cu(A), act))
+            assert _bits_equal(out, ref_pipe)
     step = max(1, M // 400)
     rows = np.unique(np.concatenate([np.arange(0, M, step), np.arange(max(0, M - 130), M)]))
     ref, _ = O.layer_per_token_i8(A[rows], q, s, zps, b, sumW, code)
