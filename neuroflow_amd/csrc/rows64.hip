@@ -18,17 +18,17 @@ template <bool FP8, int ACT, bool RES, int XQ, bool FIXED = false>
 static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
     auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES, XQ, FIXED>;
     static const int per_cu = resident_blocks(kern);
-    // Persistent waves that all take the same number of tiles (to within
-    // one): the fewest waves that keep the per-wave count of a full grid.
-    // When a full grid would give each wave 8 tiles or more, twice as many
-    // waves are launched (the later ones start as resident blocks finish):
-    // more rows in flight and a shorter tail, while every wave still
-    // amortises its weight / constant setup over >= 4 tiles (measured: +3.5%
-    // at 1 Mi rows; at 256 Ki rows, 2 tiles per wave lost 6%).
+    // Waves that all take the same number of tiles (to within one): the
+    // fewest tiles per wave that a full grid of resident waves allows, but at
+    // most 4 -- larger layers launch more waves than are resident, and the
+    // later ones start as earlier ones finish.  Measured at K = N = 64 with
+    // GELU, 1 Mi rows: 4 tiles per wave 85.4 us, 7 (a full grid doubled)
+    // 89.0 us, 8 86.8 us; 256 Ki rows: 4 -> 23.8-24.1 us, 2 -> 25.3 us,
+    // 6 -> 26.0 us; 32 Ki rows: 1 -> 7.5 us.  Fewer tiles per wave pay the
+    // per-wave weight and constant setup more often; more leave a longer tail.
     const int64_t tiles = (a.M + 15) / 16;
-    int64_t slots = static_cast<int64_t>(num_cus()) * per_cu * 4;
-    if (tiles >= 8 * slots) slots *= 2;
-    const int64_t per_wave = (tiles + slots - 1) / slots;
+    const int64_t slots = static_cast<int64_t>(num_cus()) * per_cu * 4;
+    const int64_t per_wave = std::min<int64_t>(4, (tiles + slots - 1) / slots);
     const int64_t waves = (tiles + per_wave - 1) / per_wave;
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, st, a);
 }
