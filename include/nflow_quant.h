@@ -99,8 +99,9 @@ const char* nflow_last_error(void);
  * "no_gemm", "no_rows64", "no_token_gemm", "gemm_reg" (0 / 1) and
  * "gemm_tile" (0 = the launcher's choice, else 88, 48, 44, 24 or 22) and
  * "gemm_mfma" (0 = the launcher's choice, else 16 or 32: the MFMA shape of
- * the LDS-DMA GEMM) and "no_wide" (0 / 1: keep K = 512 / 1024 layers off the
- * persistent GEMM).  The
+ * the LDS-DMA GEMM), "no_wide" (0 / 1: keep K = 512 / 1024 layers off the
+ * persistent GEMM) and "no_rows64_queue" (0 / 1: the K = N = 64 layer with
+ * its static tile deal instead of the per-CU tile queue).  The
  * environment variables NFLOW_<NAME> set the initial values, read once at
  * the library's first launch.  Process-wide; *previous (if not NULL)
  * receives the value replaced.  Unknown names return NFLOW_INVALID_ARG. */

@@ -165,9 +165,17 @@ __device__ __attribute__((noinline)) uint32_t pack4_token_scale(v4f v, float s) 
 // for every row (QuantiseActivation, int8_gemm.cpp:507-520, as
 // LinearForwardBatched and LinearForward run it) instead of the per-row
 // absmax; the epilogue's integer formula is a.formula's.
-template <bool FP8, int ACT, int PF = 1, bool RES = false, int XQ = 0, bool FIXED = false>
-__global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
+// WPB: waves per block.  4: blocks of 4 waves, wave w takes tiles w,
+// w + nwaves, ... (a static, balanced deal).  16: one block per CU whose 16
+// waves share the block's tiles through an LDS counter: a wave takes the
+// next tile when it starts one, so waves whose loads are served late take
+// fewer tiles (with the static deal the slowest waves of a 256 Ki-row layer
+// finished 7 us after the median wave).
+template <bool FP8, int ACT, int PF = 1, bool RES = false, int XQ = 0, bool FIXED = false, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs a) {
     static_assert(!(FIXED && FP8), "the fixed-scale mode is INT8");
+    static_assert(WPB == 4 || (WPB == 16 && PF == 1), "block shapes");
+    constexpr bool QUEUE = WPB == 16;
     constexpr bool INT_EPI = !FP8;
     using L = Rows64Lds<FP8>;
     const int lane = threadIdx.x & 63;
@@ -175,14 +183,19 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     const int r = lane & 15;       // MFMA layout
     const int g = lane >> 4;
     const int lr = lane >> 4;      // linear layout: row within a 4-row group
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid;
-    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * WPB + wid;
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * WPB;
     const int64_t ntiles = (a.M + 15) >> 4;
+    // QUEUE: this block's tiles are blockIdx.x + G k (G blocks), as in the
+    // static deal; the first WPB (k = wid) dealt one per wave, the rest taken
+    // through q_next.
+    const int64_t qG = gridDim.x;
     const int64_t M = a.M;
     const int lin_off = lane * 16;  // byte offset of the lane in a 4-row group
     constexpr int DW = FP8 ? 8 : 4;  // operand dwords per lane
 
-    __shared__ L lds[4];
+    __shared__ L lds[WPB];
+    __shared__ int q_next;
     __shared__ IntEpi lds_e[INT_EPI ? 64 : 1];
     __shared__ uint32_t lds_w[FP8 ? 64 * W_BF16_STRIDE : 1];
     __shared__ v4f lds_sw[16];
@@ -200,7 +213,7 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             x[j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, lin_off + 1024 * j, 0, kCpolNt));
     };
 
-    int64_t tile = wave;
+    int64_t tile = QUEUE ? static_cast<int64_t>(blockIdx.x) + qG * wid : wave;
     v4f pre[PF][4];
 
     // Setup loads first -- the weights, the per-column constants and the
@@ -217,9 +230,11 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     int32_t zpw_c[4] = {0, 0, 0, 0}, sumw_c[4] = {0, 0, 0, 0};   // column 16 nt + r
     uint32_t w8[4];
     if constexpr (FP8) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (threadIdx.x >> 2) * 64 + 16 * (threadIdx.x & 3));
+        if (threadIdx.x < 256) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (threadIdx.x >> 2) * 64 + 16 * (threadIdx.x & 3));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) w8[q] = src[q];
+            for (int q = 0; q < 4; ++q) w8[q] = src[q];
+        }
     } else {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
@@ -245,12 +260,14 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     }
     bool triv[4] = {true, true, true, true};
     if constexpr (FP8) {
-        const int n = threadIdx.x >> 2, c = threadIdx.x & 3;
-        uint32_t o[8];
-        bytes_to_bf16_op(w8, o);
-        v4u* dst = reinterpret_cast<v4u*>(lds_w + n * W_BF16_STRIDE + 8 * c);
-        dst[0] = v4u{o[0], o[1], o[2], o[3]};
-        dst[1] = v4u{o[4], o[5], o[6], o[7]};
+        if (threadIdx.x < 256) {
+            const int n = threadIdx.x >> 2, c = threadIdx.x & 3;
+            uint32_t o[8];
+            bytes_to_bf16_op(w8, o);
+            v4u* dst = reinterpret_cast<v4u*>(lds_w + n * W_BF16_STRIDE + 8 * c);
+            dst[0] = v4u{o[0], o[1], o[2], o[3]};
+            dst[1] = v4u{o[4], o[5], o[6], o[7]};
+        }
     } else {
         // The epilogue constants of column 16 nt + r (row_sum4 reduces the
         // four k-groups' byte sums; K = 64, so the dot covers every k).
@@ -272,9 +289,10 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
     // every element takes the exact quotient).
     const float fixed_inv = FIXED ? 1.0f / a.scale_A : 0.0f;
     const bool fixed_exact = FIXED && !(a.scale_A >= 0x1p-120f && a.scale_A <= 0x1p120f);
+    if (QUEUE && threadIdx.x == 0) q_next = WPB;
     __syncthreads();
 
-    for (; tile < ntiles; tile += nwaves) {
+    while (tile < ntiles) {
         v4f x[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) x[j] = pre[0][j];
@@ -282,7 +300,17 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
         for (int p = 0; p + 1 < PF; ++p)
 #pragma unroll
             for (int j = 0; j < 4; ++j) pre[p][j] = pre[p + 1][j];
-        load_lin(tile + PF * nwaves, pre[PF - 1]);
+        // The next tile (a tile at or past the end loads zeros: its rows are
+        // outside the buffer range).
+        int64_t next;
+        if constexpr (QUEUE) {
+            int k = 0;
+            if (lane == 0) k = atomicAdd(&q_next, 1);
+            next = static_cast<int64_t>(blockIdx.x) + qG * __builtin_amdgcn_readfirstlane(k);
+        } else {
+            next = tile + nwaves;
+        }
+        load_lin(next + (PF - 1) * nwaves, pre[PF - 1]);
         // Residual tile in the MFMA result layout: lane (r, g), column tile
         // nt -> row r, columns 16 nt + 4 g .. + 3.
         // Position of row r for the per-position x2 fake-quant.
@@ -513,6 +541,7 @@ __global__ __launch_bounds__(256, 3) void k_rows64(RowsArgs a) {
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, y[j]), rs, lin_off + 1024 * j, 0, NFQ_ROWS64_STORE_CPOL);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        tile = next;
     }
 }
 

@@ -193,3 +193,69 @@ def test_fno_layer_x2_fake_quant_on_handles_and_errors(gpu):
             h(_cu(x), "relu", residual=_cu(x1), x2_quant=q)
         assert e.value.code == code
     h.close()
+
+
+# ---- the K = N = 64 kernel's per-CU tile queue ---------------------------------
+
+@pytest.fixture
+def _queue_off():
+    """Context: the K = 64 kernel with its static tile deal
+    (nflow_debug_set_kernel_path("no_rows64_queue", 1))."""
+    import contextlib
+    import ctypes
+
+    from neuroflow_amd import _lib
+
+    @contextlib.contextmanager
+    def ctx():
+        L = _lib.lib()
+        prev = ctypes.c_int(0)
+        _lib.check(L.nflow_debug_set_kernel_path(b"no_rows64_queue", 1, ctypes.byref(prev)), "path")
+        try:
+            yield
+        finally:
+            _lib.check(L.nflow_debug_set_kernel_path(b"no_rows64_queue", prev.value, None), "path")
+    return ctx
+
+
+@pytest.mark.parametrize("M", [262144 + 37, 1 << 20])
+@pytest.mark.parametrize("form", ["int8_gelu", "int8_none", "fp8_gelu", "fno_relu", "fno_x2q", "batched"])
+def test_rows64_tile_queue_matches_static_deal(gpu, _queue_off, M, form):
+    """Layers of 256 Ki+ rows run on one 16-wave block per CU whose waves take
+    tiles from an LDS counter; every output equals the static deal's bit for
+    bit (each tile is computed once, by whichever wave takes it), and sampled
+    rows equal the oracle."""
+    N = K = 64
+    W = WL.uniform(90, (N, K), -0.125, 0.125)
+    b = WL.uniform(91, (N,), -0.1, 0.1)
+    h = WL.normal(92, (M, K))
+    h[M // 3] = np.nan
+    s = O.per_channel_scales(W, 127.0)
+    q, sw = O.quantise_weight_2d(W, s)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(np.zeros(N, np.int32)), _cu(b), sum_W_per_row=_cu(sw))
+    x1 = _cu((0.5 * WL.normal(93, (M, N))).astype(np.float32)) if form.startswith("fno") else None
+    hd = _cu(h)
+
+    def run():
+        if form == "int8_gelu":
+            return Q.linear_forward_per_token(p, hd, "gelu")
+        if form == "int8_none":
+            return Q.linear_forward_per_token(p, hd, "none")
+        if form == "fp8_gelu":
+            return Q.Fp8Linear(W, b)(hd, "gelu")
+        if form == "fno_relu":
+            return Q.fno_layer_per_token(p, hd, x1, "relu")
+        if form == "fno_x2q":
+            return Q.fno_layer_per_token(p, hd, x1, "gelu", x2_quant=Q.X2Quant("per_tensor", scale=0.031, zero_point=-4))
+        pb = Q.Int8LinearParams(_cu(q), _cu(s), _cu(np.zeros(N, np.int32)), _cu(b), scale_A=0.021, zp_A=3)
+        return Q.linear_forward_batched(pb, hd)
+
+    y = _host(run())
+    with _queue_off():
+        y_static = _host(run())
+    assert _same(y, y_static)
+    if form == "int8_none":
+        rows = np.unique(np.concatenate([np.arange(0, M, 997), [M // 3, M - 1]]))
+        ref, _ = O.layer_per_token_i8(h[rows], q, s, None, b, sw, 0)
+        fin = np.isfinite(ref)
+        assert _same(y[rows][fin], ref[fin])
