@@ -55,6 +55,10 @@ def parse():
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch", "fno1d", "fno2d"])
     ap.add_argument("--sets", type=int, default=0, help="buffer sets to rotate (0 = auto)")
+    ap.add_argument("--prewarm-ms", type=float, default=100.0,
+                    help="before the warm-up steps, repeat the workload's steps for this much wall "
+                         "time so that the timed steps run at the clocks a sustained load settles at "
+                         "(0 = off); reported as \"prewarm\"")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="measure only --workload (by default every other configuration is measured "
@@ -92,8 +96,8 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     that Python overhead stays off the GPU's critical path.  The layer's
     weights are per-channel symmetric (zero points 0, sum_W equal to the
     codes' own sums), so the struct leaves zp_W and sum_W out: the GEMM then
-    needs no byte sums and runs the same LDS-DMA kernel as the layer, with
-    identical outputs."""
+    needs no byte sums of its own and runs the same GEMM kernel as the
+    layer, with identical outputs."""
     import ctypes as C
     import dataclasses
 
@@ -216,6 +220,8 @@ def _kernel_of(wl):
     if (wl.layers[0].fmt == "int8" and all(l.W.shape[1] in (128, 256, 512) and l.W.shape[0] % 64 == 0
                                            for l in wl.layers)):
         return "nfq::k_token_gemm"    # the whole per-token layer in one launch
+    if K0 in (512, 1024) and N0 % 4 == 0 and wl.layers[0].fmt == "int8":
+        return "nfq::k_gemm_wide"     # persistent GEMM after a per-token quantise launch
     if K0 % 64 == 0 and K0 >= 128 and wl.layers[0].fmt == "int8":
         return "nfq::k_gemm_pipe"     # after a per-token quantise launch
     return "nfq::k_rows"
@@ -280,6 +286,20 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
             kind, k = srcs[l]
             src = b["in"][k] if kind == "input" else b["out"][k]
             run(src.data_ptr(), b["out"][l].data_ptr(), M, sp)
+
+    # Device pre-warm: the same steps for at least `args.prewarm_ms` of wall
+    # time, in batches that double in size (a synchronize after each), ahead of
+    # the `warmup` steps.  The GPU and its memory start a run at idle clocks:
+    # at C2, 5-10 warm-up steps leave the timed layers at 25-26 us, against
+    # 23.5 us after 50 ms of load.
+    pw_steps, pw_t0, batch = 0, time.perf_counter(), 4
+    while args.prewarm_ms > 0 and (time.perf_counter() - pw_t0) * 1e3 < args.prewarm_ms:
+        for _ in range(batch):
+            step(pw_steps)
+            pw_steps += 1
+        torch.cuda.synchronize()
+        batch = min(2 * batch, 4096)
+    pw_ms = (time.perf_counter() - pw_t0) * 1e3 if pw_steps else 0.0
 
     for i in range(warmup):
         step(i)
@@ -357,7 +377,7 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
                  "bytes_per_launch": bytes_step // len(layers),
                  "ops_per_launch": ops_step // len(layers),
                  "tops": round(tops, 2), "gbs": round(gbs, 1)})
-    if kernel == "nfq::k_gemm_pipe":
+    if kernel in ("nfq::k_gemm_pipe", "nfq::k_gemm_wide"):
         # The layer is two launches (quantise, then the GEMM); the roofline
         # is the GEMM kernel's own, timed alone on layer 0's shape.
         g_us, g_bytes, g_ops = time_gemm_only(wl, layers, sets, stream, max(20, steps))
@@ -401,7 +421,8 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
         except Exception as e:  # reported, not fatal: the GPU figure stands alone
             cpu = {"error": f"{type(e).__name__}: {e}"}
 
-    rec = {"wl": wl, "n_sets": n_sets, "graphs": graphs is not None, "ms_per_step": ms_per_step,
+    rec = {"wl": wl, "n_sets": n_sets, "graphs": graphs is not None,
+           "prewarm": {"steps": pw_steps, "ms": round(pw_ms, 1)}, "ms_per_step": ms_per_step,
            "value": wl.samples / (ms_per_step * 1e-3), "roofline": roof, "parity": parity, "cpu": cpu,
            "copy": copy, "gen_s": t_gen}
     del sets, layers
@@ -559,7 +580,7 @@ def _config_entry(name, rec):
     wl, roof = rec["wl"], rec["roofline"]
     e = {"workload": wl.name, "rows": wl.M, "layers": len(wl.layers),
          "ms_per_step": round(rec["ms_per_step"], 5), "samples_per_s": round(rec["value"], 2),
-         "dtype": wl.layers[0].fmt}
+         "dtype": wl.layers[0].fmt, "prewarm": rec["prewarm"]}
     e.update({k: roof[k] for k in ("bound", "kernel", "kernel_avg_us", "achieved", "unit", "frac", "tops", "gbs",
                                    "bytes_per_launch", "ops_per_launch", "traffic")})
     if "layer_avg_us" in roof:
@@ -619,6 +640,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": rec["prewarm"],
         "ms_per_step": round(rec["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
