@@ -95,11 +95,10 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     region; launches go through the C entry point with a prebuilt struct so
     that Python overhead stays off the GPU's critical path.  The layer's
     weights are per-channel symmetric (zero points 0, sum_W equal to the
-    codes' own sums), so the struct leaves zp_W and sum_W out: the GEMM then
-    needs no byte sums of its own and runs the same GEMM kernel as the
-    layer, with identical outputs."""
+    codes' own sums), so the struct leaves zp_W and sum_W out, as the
+    layer's own per-token calls do: the same GEMM kernel as in the layer,
+    with identical outputs."""
     import ctypes as C
-    import dataclasses
 
     import torch
     from neuroflow_amd import _lib
@@ -110,7 +109,7 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     codes = [Q.quantise_per_token(s_["in"][k]) for s_ in sets]
     outs = [torch.empty(M, N, dtype=torch.float32, device=sets[0]["in"][0].device) for _ in sets]
     assert not obj.params.zp_W.any().item()
-    ps = dataclasses.replace(obj.params, zp_W=None, sum_W_per_row=None).c_struct()
+    ps = obj.token_params.c_struct()
     fn = _lib.lib().nflow_int8_linear_forward_quantised
     act = {"none": 0, "relu": 1, "gelu": 2}[L.act]
     sptr = stream.cuda_stream

@@ -27,8 +27,9 @@
 //    lane straight into LDS); 8 lanes cover one row's whole 128-byte line, so
 //    every instruction reads 8 full cache lines (with 64-byte steps each
 //    instruction read 16 half lines, and the loads alone took 50 us of a
-//    65536 x 1024 x 1024 GEMM).  Three stages, loaded two steps ahead; the
-//    load stream runs across tile boundaries.
+//    65536 x 1024 x 1024 GEMM).  Three stages loaded two steps ahead (four,
+//    three ahead, with 128 x 128 tiles); the load stream runs across tile
+//    boundaries.
 //  - Per-tile tables (scale_W, bias, row scales and the integer-epilogue
 //    inputs) arrive by LDS DMA with the tile's first step, double-buffered
 //    by tile parity; they are read one tile later, by the drain.
@@ -68,8 +69,12 @@ struct WideCfg {
     static constexpr int BM = 32 * TI * WM, BN = 32 * TJ * WN;
     static constexpr int ROW = 128;                          // bytes of K per stage row
     static constexpr int STAGE = (BM + BN) * ROW;            // 48 KB / 32 KB
-    static constexpr int NS = 3;                             // LDS stages
-    static constexpr int LEAD = 2;                           // load lead (steps)
+    // LDS stages and the load lead in steps: three stages two steps ahead
+    // fill the LDS at 128 x 256 (144 KB with the tables); 128 x 128 tiles
+    // take a fourth stage, three steps ahead (a CU's L2 -> LDS rate grows
+    // with the loads in flight).
+    static constexpr int NS = TJ == 1 ? 4 : 3;
+    static constexpr int LEAD = NS - 1;
     static constexpr int NL = (BM + BN) / 8 / WAVES;         // 1 KB loads per wave per step (8 rows each)
     static constexpr int VALS = TI * TJ * 16;                // accumulator values per lane
 };
@@ -192,7 +197,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     constexpr int STORES = 4 * PER_STEP;
     static_assert(Cf::VALS % (4 * NK) == 0 && PER_STEP >= 1 && NK >= 2, "epilogue split over the K steps");
     static_assert(wide_wait(0, NK, NL, NTAB, STORES, Cf::LEAD) < 64 &&
-                  wide_wait(1, NK, NL, NTAB, STORES, Cf::LEAD) < 64, "vmcnt field");
+                  wide_wait(1, NK, NL, NTAB, STORES, Cf::LEAD) < 64 &&
+                  wide_wait(2, NK, NL, NTAB, STORES, Cf::LEAD) < 64, "vmcnt field");
+    static_assert(Cf::LEAD < NK && Cf::NS == Cf::LEAD + 1, "stage ring");
     __shared__ __attribute__((aligned(16))) uint8_t stages[Cf::NS][Cf::STAGE];
     __shared__ __attribute__((aligned(16))) WideTables tb[2];
 
@@ -292,9 +299,30 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     // c1 = -2 zp_W and, for the row-VNNI formula with a caller's sum_W,
     // c0 = 128 (W-row byte sum - sum_W): the forms of int_epi_consts), then
     // the reference's dequantise order.
-    auto drain = [&](const Acc& acc, int par, const WideTile& t, auto slc) {
+    //
+    // The lane's TJ columns' constants are read from the tables once per tile
+    // (slice 0) into registers.
+    struct ColC {
+        float sw[TJ], bb[TJ];
+        int32_t c0[TJ], c1[TJ];
+    };
+    auto col_consts = [&](const WideTables& T_, ColC& cc) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int col = 32 * TJ * wn + 32 * j + lr;
+            cc.sw[j] = T_.sw[col];
+            cc.bb[j] = T_.bias[col];
+            if constexpr (INT_EPI) {
+                cc.c1[j] = static_cast<int32_t>(0u - 2u * static_cast<uint32_t>(T_.zpw[col]));
+                cc.c0[j] = static_cast<int32_t>(128u * (static_cast<uint32_t>(T_.c0a[col]) -
+                                                        static_cast<uint32_t>(T_.c0b[col])));
+            }
+        }
+    };
+    auto drain = [&](const Acc& acc, int par, const WideTile& t, ColC& cc, auto slc) {
         constexpr int sl = decltype(slc)::value;
         const WideTables& T_ = tb[par];
+        if constexpr (sl == 0) col_consts(T_, cc);
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const auto rs = wide_rsrc(static_cast<float*>(a.C) + t.m0 * N, rows * N * 4);
 #pragma unroll
@@ -303,14 +331,6 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             const int i = vi / (16 * TJ), j = (vi / 16) % TJ, q = (vi % 16) / 4;
             const int col = 32 * TJ * wn + 32 * j + lr;       // within the block tile
             const int row0 = 32 * TI * wm + 32 * i + 4 * lg + 8 * q;
-            const float sw = T_.sw[col], bb = T_.bias[col];
-            int32_t c0 = 0, c1 = 0;
-            bool triv = true;
-            if constexpr (INT_EPI) {
-                c1 = static_cast<int32_t>(0u - 2u * static_cast<uint32_t>(T_.zpw[col]));
-                c0 = static_cast<int32_t>(128u * (static_cast<uint32_t>(T_.c0a[col]) - static_cast<uint32_t>(T_.c0b[col])));
-                triv = __builtin_amdgcn_ballot_w64(c0 != 0 || c1 != 0) == 0;
-            }
             const uint32_t voff0 = t.n0 + col < N ? static_cast<uint32_t>((row0 * N + t.n0 + col) * 4) : 0x80000000u;
             const v4f sa = *reinterpret_cast<const v4f*>(T_.sa + row0);
             v4i sa_i = {0, 0, 0, 0};
@@ -319,13 +339,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             for (int e = 0; e < 4; ++e) {
                 const int32_t d = acc[i][j][4 * q + e];
                 float tv;
-                if (!INT_EPI || triv) {
+                if constexpr (INT_EPI)
+                    tv = static_cast<float>(static_cast<int32_t>(static_cast<uint32_t>(d) + static_cast<uint32_t>(cc.c0[j]) +
+                                                                 static_cast<uint32_t>(cc.c1[j]) * static_cast<uint32_t>(sa_i[e])));
+                else
                     tv = static_cast<float>(d);
-                } else {
-                    tv = static_cast<float>(static_cast<int32_t>(static_cast<uint32_t>(d) + static_cast<uint32_t>(c0) +
-                                                                 static_cast<uint32_t>(c1) * static_cast<uint32_t>(sa_i[e])));
-                }
-                const float y = activate<ACT>(dequant_bias(sw, sa[e], tv, bb));
+                const float y = activate<ACT>(dequant_bias(cc.sw[j], sa[e], tv, cc.bb[j]));
                 // Non-temporal store (cache policy nt).
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), rs,
                                                       static_cast<int>(voff0 + static_cast<uint32_t>(e * N * 4)), 0, 2);
@@ -339,21 +358,21 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     // the stage that step k + LEAD overwrites), the loads of step k + LEAD
     // (the next tile's past the end), the tile's own tables at k = 0, the
     // MFMAs, then slice k of the previous tile's epilogue.  The prologue
-    // issues steps 0 and 1, each followed by STORES stores to a zero-byte
-    // range: the instruction sequence of a tile's last two steps, so that the
-    // first tile's waits count right.  (Every wait counts this wave's vector
+    // issues steps 0 .. LEAD - 1, each followed by STORES stores to a
+    // zero-byte range: the instruction sequence of a tile's last LEAD steps,
+    // so that the first tile's waits count right.  (Every wait counts this wave's vector
     // memory instructions exactly; the drain's stores go to rows N floats
     // apart, N unknown at compile time, so they cannot be merged either.)
     WideTile cur = wide_tile<BM, BN>(0, ntiles, n_tiles_n);
     if (!cur.valid) return;
     {
         const v4u none = wide_desc(nullptr, 0);
-        dma_step(st_base, cur, 0);
 #pragma unroll
-        for (int q = 0; q < STORES; ++q) wide_null_store(none, 4 * q);
-        dma_step(st_base + Cf::STAGE, cur, 1);
+        for (int k = 0; k < Cf::LEAD; ++k) {
+            dma_step(st_base + Cf::STAGE * k, cur, k);
 #pragma unroll
-        for (int q = 0; q < STORES; ++q) wide_null_store(none, 4 * q);
+            for (int q = 0; q < STORES; ++q) wide_null_store(none, 4 * q);
+        }
     }
     WideTile prev{0, 0, false};
     int sc = 0;   // stage of the current step: the global step number mod NS
@@ -364,6 +383,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j) acc[i][j] = v16i_w_t{};
+        ColC cc;
         wide_static_for(std::make_integer_sequence<int, NK>{}, [&](auto kc) {
             constexpr int k = decltype(kc)::value;
             const int sl = sc + Cf::LEAD >= Cf::NS ? sc + Cf::LEAD - Cf::NS : sc + Cf::LEAD;
@@ -384,7 +404,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
                 if (hh + 2 < 4) frag_read(st, hh + 2, xf[hh + 2], wf[hh + 2]);
                 mfma_part(acc, xf[hh], wf[hh]);
             }
-            drain(pacc, par ^ 1, pt, kc);
+            drain(pacc, par ^ 1, pt, cc, kc);
             sc = sc + 1 == Cf::NS ? 0 : sc + 1;
         });
     };
@@ -404,7 +424,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             // accA holds the last tile (parity 0).
             __builtin_amdgcn_s_waitcnt(0x070);
             asm volatile("s_barrier" ::: "memory");
-            wide_static_for(std::make_integer_sequence<int, NK>{}, [&](auto sc2) { drain(accA, 0, prev, sc2); });
+            ColC cc;
+            wide_static_for(std::make_integer_sequence<int, NK>{}, [&](auto sc2) { drain(accA, 0, prev, cc, sc2); });
             return;
         }
         nxt = wide_tile<BM, BN>(it + 1, ntiles, n_tiles_n);
@@ -415,7 +436,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
         if (!cur.valid) {
             __builtin_amdgcn_s_waitcnt(0x070);
             asm volatile("s_barrier" ::: "memory");
-            wide_static_for(std::make_integer_sequence<int, NK>{}, [&](auto sc2) { drain(accB, 1, prev, sc2); });
+            ColC cc;
+            wide_static_for(std::make_integer_sequence<int, NK>{}, [&](auto sc2) { drain(accB, 1, prev, cc, sc2); });
             return;
         }
     }

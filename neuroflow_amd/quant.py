@@ -11,6 +11,7 @@ failed Status into RuntimeError (pybind_module.cpp:189-191).
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 from dataclasses import dataclass
 from typing import Optional
 
@@ -437,15 +438,20 @@ class Int8Linear:
             bias=None if bias is None else torch.from_numpy(np.ascontiguousarray(bias, np.float32)).to(dev),
             sum_W_per_row=torch.from_numpy(sum_w).to(dev))
         self.W_q, self.scale_W, self.sum_W = q, scales, sum_w
+        # The per-token calls pass neither the zero points (all 0) nor sum_W
+        # (each row's code sum): the same outputs bit for bit, without the
+        # kernels' integer-epilogue terms.
+        assert np.array_equal(sum_w, q.sum(axis=1, dtype=np.int64))
+        self.token_params = dataclasses.replace(self.params, zp_W=None, sum_W_per_row=None)
 
     def __call__(self, x: torch.Tensor, activation="gelu", out=None) -> torch.Tensor:
-        return linear_forward_per_token(self.params, x, activation, out=out)
+        return linear_forward_per_token(self.token_params, x, activation, out=out)
 
     def launcher(self, activation="gelu"):
         """A prepared call for a hot loop: `run(x_ptr, out_ptr, M, stream)`
         with raw device pointers, the C struct built once.  The caller keeps
         x / out alive and shaped (M, in_features) / (M, out_features)."""
-        ps = self.params.c_struct()
+        ps = self.token_params.c_struct()
         fn = _lib.lib().nflow_int8_linear_forward_per_token
         ref = C.byref(ps)
         act = _act(activation)
