@@ -6,7 +6,9 @@
 namespace nfq {
 
 bool token_gemm_ok(const RowsArgs& a) {
-    return (a.K == 128 || a.K == 256 || a.K == 512) && a.N % 64 == 0 && a.N > 0 && aligned(a.A, 16) &&
+    // N <= 2^24 keeps a 16-row output strip's byte count inside a buffer range.
+    return (a.K == 128 || a.K == 256 || a.K == 512) && a.N % 64 == 0 && a.N > 0 && a.N <= (1 << 24) &&
+           aligned(a.A, 16) &&
            aligned(a.C, 16) && aligned(a.W, 16);
 }
 

@@ -39,9 +39,10 @@
 //    stores are dropped), so each wait's vmcnt is a compile-time count.  The
 //    loads are inline asm, which the compiler does not track; it would
 //    otherwise also wait for the drain's stores before reading a stage.
-//  - Output stores are non-temporal: the 256 MiB of a trunk layer's output
-//    would otherwise displace the L2-resident weight and code lines the
-//    loads reuse (measured: 146 -> 114 us at 65536 x 1024 x 1024).
+//  - Output stores are non-temporal and written through the L2 (nt | sc1):
+//    the 256 MiB of a trunk layer's output would otherwise displace the
+//    L2-resident weight and code lines the loads reuse (measured: 146 -> 114
+//    us at 65536 x 1024 x 1024 with nt; 81 us now, with sc1 too).
 //  - Tiles are dealt so that at any time each XCD works on a contiguous
 //    range of tiles: the BN-column tiles of one row tile share that XCD's L2.
 #pragma once
@@ -53,6 +54,12 @@
 #include "rows_kernel.h"
 
 namespace nfq {
+
+// Cache policy of the output stores: nt | sc1 (non-temporal, written
+// through the L2).  Measured at 65536 x 1024 x 1024: 81.0 us, against 84-86
+// with nt alone, 113 with sc1 alone and 119 with neither; at 4096 x 1024 x
+// 1024: 11.0 us against 11.3-11.6 / 11.0 / 12.5.
+constexpr int kWideStoreCpol = 2 | 16;
 
 typedef int v16i_w_t __attribute__((ext_vector_type(16)));
 
@@ -345,9 +352,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
                 else
                     tv = static_cast<float>(d);
                 const float y = activate<ACT>(dequant_bias(cc.sw[j], sa[e], tv, cc.bb[j]));
-                // Non-temporal store (cache policy nt).
                 __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y), rs,
-                                                      static_cast<int>(voff0 + static_cast<uint32_t>(e * N * 4)), 0, 2);
+                                                      static_cast<int>(voff0 + static_cast<uint32_t>(e * N * 4)), 0, kWideStoreCpol);
             }
         }
     };
