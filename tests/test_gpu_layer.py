@@ -58,6 +58,36 @@ def test_layer_from_int8_blob_with_zero_points(gpu):
         assert _same(out, ref)
 
 
+@pytest.mark.parametrize("K,N", [(64, 64), (256, 256), (1024, 512)])
+def test_layer_symmetric_blob_detection(gpu, K, N):
+    """A handle built from a symmetric blob (zero points 0, sum_W the code
+    sums) runs its per-token calls without the integer-epilogue terms; a
+    blob with one nonzero zero point, or with a sum_W that differs from the
+    code sums, keeps them.  Each output equals the oracle with the blob as
+    given, bit for bit (no activation), on the K = 64, one-pass and
+    persistent-GEMM kernels."""
+    M = 700
+    W = WL.uniform(69, (N, K), -0.125, 0.125)
+    s = O.per_channel_scales(W, 127.0)
+    zps = np.zeros(N, np.int32)
+    q, sw = O.quantise_weight_2d(W, s, zps)
+    b = WL.uniform(70, (N,), -0.1, 0.1)
+    A = WL.normal(71, (M, K))
+    sw_off = (sw + np.arange(N, dtype=np.int32) % 5 - 2).astype(np.int32)
+    zp_one = zps.copy()
+    zp_one[N // 3] = 2
+    outs = []
+    for zp_b, sw_b in ((zps, sw), (zps, sw_off), (zp_one, sw)):
+        layer = Q.Layer.from_int8_blob(q, s, zp_b, b, sw_b)
+        out = _host(layer(_cu(A), "none"))
+        layer.close()
+        ref, _ = O.layer_per_token_i8(A, q, s, zp_b, b, sw_b, 0)
+        assert _same(out, ref)
+        outs.append(out)
+    # The terms show: the nonsymmetric blobs give other outputs.
+    assert not _same(outs[1], outs[0]) and not _same(outs[2], outs[0])
+
+
 def test_layer_create_destroy_cycles(gpu):
     W = WL.kaiming_uniform(67, 64, 64)
     x = _cu(WL.normal(68, (128, 64)))
