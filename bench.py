@@ -97,7 +97,13 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     weights are per-channel symmetric (zero points 0, sum_W equal to the
     codes' own sums), so the struct leaves zp_W and sum_W out, as the
     layer's own per-token calls do: the same GEMM kernel as in the layer,
-    with identical outputs."""
+    with identical outputs.  Back to back, the 1024-wide trunk GEMMs reach
+    the chip's power limit after ~1.5 ms (86-90 us per launch, then ~108
+    us), so this average sits a little above the same kernel's duration in
+    the layer chain, where a quantise launch separates them (a median of
+    ~84 us in the kernel trace); the time of an event recorded between the
+    two launches of a layer is taken before the quantise has finished, so
+    events cannot bracket the GEMM inside the chain."""
     import ctypes as C
 
     import torch
