@@ -198,13 +198,15 @@ struct Tile {
     int t0, c0;
 };
 
+// Tile `id` of TT tokens x 64 channels.
+template <int TT>
 __device__ __forceinline__ bool tile_of(int64_t id, int64_t samples, int n, int w, Tile& tl) {
-    const int tt = (n + 63) / 64, tc = (w + 63) / 64;
+    const int tt = (n + TT - 1) / TT, tc = (w + 63) / 64;
     const int64_t per_sample = static_cast<int64_t>(tt) * tc;
     if (id >= samples * per_sample) return false;
     tl.s = id / per_sample;
     const int rem = static_cast<int>(id % per_sample);
-    tl.t0 = (rem / tc) * 64;
+    tl.t0 = (rem / tc) * TT;
     tl.c0 = (rem % tc) * 64;
     return true;
 }
@@ -246,14 +248,15 @@ __device__ __forceinline__ void stage_steps(float* steps, const float* thr) {
     __syncthreads();
 }
 
+template <int TT>
 __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, int64_t samples, int n, int w,
                                                           FakeQuant fq) {
-    __shared__ float tile[64][65];
+    __shared__ float tile[64][TT + 1];
     __shared__ float steps[16];
     stage_steps(steps, fq.thr);
     Tile tl;
-    for (int64_t id = blockIdx.x; tile_of(id, samples, n, w, tl); id += gridDim.x) {
-        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, samples, n, w, tl); id += gridDim.x) {
+        for (int i = threadIdx.x; i < TT * 64; i += 256) {
             const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) {
                 const int64_t o = (tl.s * n + t) * w + c;
@@ -263,8 +266,8 @@ __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, i
             }
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) hc[(tl.s * w + c) * n + t] = tile[cr][tr];
         }
         __syncthreads();
@@ -568,20 +571,21 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
 // The snaps read their step tables from LDS, one entry per element
 // (snap_exponent_binade); the runtime checks the one-step-per-binade layout
 // of the table at creation.
+template <int TT>
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
-    __shared__ float tx1[64][65];  // x1, then (in place, same thread) the new h
+    __shared__ float tx1[64][TT + 1];  // x1, then (in place, same thread) the new h
     __shared__ float thr_x2[16], thr_next[16];
     const int n = a.n, w = a.w;
     if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
     stage_steps(thr_next, a.fq_next.thr);
     Tile tl;
-    for (int64_t id = blockIdx.x; tile_of(id, a.samples, n, w, tl); id += gridDim.x) {
-        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, w, tl); id += gridDim.x) {
+        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) tx1[cr][tr] = a.x1c[(tl.s * w + c) * n + t];
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        for (int i = threadIdx.x; i < TT * 64; i += 256) {
             const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) {
                 const int64_t o = (tl.s * n + t) * w + c;
@@ -600,8 +604,8 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
             }
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-            const int cr = i / 64, tr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) a.hc[(tl.s * w + c) * n + t] = tx1[cr][tr];
         }
         __syncthreads();
@@ -650,24 +654,42 @@ hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st) {
     if (a.k == 64 && a.n >= 16 && aligned(a.x, 16) && aligned(a.W, 16)) {
         hipLaunchKernelGGL(k_linear_rows64, dim3(grid_for((rows + 3) / 4, 4, 8)), dim3(256), 0, st, a);
     } else if (a.n <= 16 && static_cast<size_t>(a.n) * a.k * sizeof(float) <= 48 * 1024) {
-        hipLaunchKernelGGL(k_linear_narrow<16>, dim3(grid_for(rows, 256, 8)), dim3(256),
-                           static_cast<size_t>(a.n) * a.k * sizeof(float), st, a);
+        // Registers for as many columns as there are (each column's sum in
+        // the same order whatever NMAX is).
+        const size_t lds = static_cast<size_t>(a.n) * a.k * sizeof(float);
+        if (a.n == 1)
+            hipLaunchKernelGGL(k_linear_narrow<1>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
+        else if (a.n <= 4)
+            hipLaunchKernelGGL(k_linear_narrow<4>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
+        else
+            hipLaunchKernelGGL(k_linear_narrow<16>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
     } else {
         hipLaunchKernelGGL(k_linear_flat, dim3(grid_for(rows * a.n, 256, 8)), dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
 
-static unsigned tile_grid(int64_t samples, int n, int w) {
-    const int64_t tiles = samples * ((n + 63) / 64) * static_cast<int64_t>((w + 63) / 64);
-    return grid_for(tiles, 1, 8);
+static int64_t tile_count(int64_t samples, int n, int w, int tt) {
+    return samples * ((n + tt - 1) / tt) * static_cast<int64_t>((w + 63) / 64);
+}
+
+// Tiles of 64 tokens, or of 8 when 64-token tiles would give fewer than two
+// blocks per CU (a small batch: one 1024-point sample of width 64 is 16
+// tiles; the tail then ran 22.7 us, its threads each taking 16 exact GELUs
+// in sequence on 16 CUs).
+static bool small_tiles(int64_t samples, int n, int w) {
+    return tile_count(samples, n, w, 64) < 2 * static_cast<int64_t>(num_cus());
 }
 
 hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,
                                    hipStream_t st) {
     if (samples <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_to_channel_major, dim3(tile_grid(samples, n, w)), dim3(256), 0, st, h, hc, samples, n, w,
-                       fq);
+    if (small_tiles(samples, n, w))
+        hipLaunchKernelGGL(k_to_channel_major<8>, dim3(grid_for(tile_count(samples, n, w, 8), 1, 8)), dim3(256), 0,
+                           st, h, hc, samples, n, w, fq);
+    else
+        hipLaunchKernelGGL(k_to_channel_major<64>, dim3(grid_for(tile_count(samples, n, w, 64), 1, 8)), dim3(256),
+                           0, st, h, hc, samples, n, w, fq);
     return hipGetLastError();
 }
 
@@ -761,7 +783,12 @@ hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t
 
 hipError_t launch_post(const PostArgs& a, hipStream_t st) {
     if (a.samples <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_post_rt, dim3(tile_grid(a.samples, a.n, a.w)), dim3(256), 0, st, a);
+    if (small_tiles(a.samples, a.n, a.w))
+        hipLaunchKernelGGL(k_post_rt<8>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 8), 1, 8)), dim3(256), 0, st,
+                           a);
+    else
+        hipLaunchKernelGGL(k_post_rt<64>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 64), 1, 8)), dim3(256), 0,
+                           st, a);
     return hipGetLastError();
 }
 
