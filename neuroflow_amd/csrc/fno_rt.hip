@@ -316,6 +316,11 @@ struct FftIo {
     int src_stride, src_rows;
     int dst_stride, dst_rows;
     bool scale;
+    // Natural-order outputs the caller keeps (0: all).  After a stage of
+    // block size B, position q feeds a kept output only if q mod B < keep, so
+    // a pass skips its groups whose in-block offset is keep or more: the
+    // kept outputs come from the same butterflies in the same order.
+    int keep;
 };
 
 template <int SRC>
@@ -363,7 +368,12 @@ __device__ __forceinline__ void fft_pass(const FftIo& io, int h0, int lane) {
     constexpr int G = 1 << P;
     const int ngroups = io.n >> P;
     const int lh0 = __builtin_ctz(static_cast<unsigned>(h0));
-    for (int gq = lane; gq < ngroups; gq += 64) {
+    // Offsets kept per block of h0 groups, and the groups that feed a kept
+    // output (all of them unless io.keep < h0).
+    const int kkn = (io.keep > 0 && io.keep < h0) ? io.keep : h0;
+    const int nneed = (ngroups >> lh0) * kkn;
+    for (int g = lane; g < nneed; g += 64) {
+        const int gq = kkn == h0 ? g : (g / kkn) * h0 + g % kkn;
         const int kk = gq & (h0 - 1);
         const int base = ((gq >> lh0) << (lh0 + P)) + kk;
         float2 v[G];
@@ -461,6 +471,7 @@ __global__ __launch_bounds__(64 * WPB) void k_rfft_modes(SpecArgs a, int64_t nlo
     io.n = n;
     io.log2n = a.log2n;
     io.modes = a.modes;
+    io.keep = a.modes;
     fft_run<1>(io, lane, 1);
 }
 
@@ -561,6 +572,7 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
     io.log2n = a.log2h;
     io.inv_n = a.inv_h;
     io.scale = INV;
+    io.keep = INV ? 0 : out_rows;
     fft_run<3>(io, lane, 3);
 }
 
