@@ -112,6 +112,47 @@ __global__ __launch_bounds__(256) void k_linear_rows64(LinArgs a) {
     }
 }
 
+// k == 64, n <= NMAX, unpadded rows: a block's 256 rows are staged in LDS by
+// coalesced loads (one thread per row reading its own 256-byte row touched
+// 64 lines per load instruction), then one thread per row as below.
+template <int NMAX>
+__global__ __launch_bounds__(256) void k_linear_narrow64(LinArgs a) {
+    __shared__ float xs[256][65];
+    __shared__ float ws[NMAX * 64];
+    const int n = a.n;
+    for (int i = threadIdx.x; i < n * 64; i += 256) ws[i] = a.W[i];
+    const int64_t rows = a.samples * a.rows_out;
+    for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * 256; r0 < rows; r0 += static_cast<int64_t>(gridDim.x) * 256) {
+        const int nr = rows - r0 < 256 ? static_cast<int>(rows - r0) : 256;
+        const v4f* x4 = reinterpret_cast<const v4f*>(a.x + r0 * 64);
+        for (int i = threadIdx.x; i < nr * 16; i += 256) {
+            const v4f v = x4[i];
+            float* d = &xs[i >> 4][(i & 15) * 4];
+            d[0] = v[0];
+            d[1] = v[1];
+            d[2] = v[2];
+            d[3] = v[3];
+        }
+        __syncthreads();
+        const int t = threadIdx.x;
+        if (t < nr) {
+            float acc[NMAX];
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j) acc[j] = (j < n && a.b) ? a.b[j] : 0.0f;
+            for (int p = 0; p < 64; ++p) {
+                const float xv = xs[t][p];
+#pragma unroll
+                for (int j = 0; j < NMAX; ++j)
+                    if (j < n) acc[j] = lin_step(acc[j], xv, ws[j * 64 + p], true);
+            }
+#pragma unroll
+            for (int j = 0; j < NMAX; ++j)
+                if (j < n) a.y[(r0 + t) * n + j] = rt_activate(acc[j], a.act);
+        }
+        __syncthreads();
+    }
+}
+
 // n <= 16: one thread per output row, all n columns in registers, W from LDS.
 template <int NMAX>
 __global__ __launch_bounds__(256) void k_linear_narrow(LinArgs a) {
@@ -164,6 +205,22 @@ __global__ __launch_bounds__(256) void k_linear_narrow(LinArgs a) {
 __global__ __launch_bounds__(256) void k_linear_flat(LinArgs a) {
     const int k = a.k, n = a.n, kplain = k - k % 8;
     const int64_t total = a.samples * a.rows_out * static_cast<int64_t>(n);
+    if (a.rows_in == a.rows_out && a.rows_valid == a.rows_out && (n & (n - 1)) == 0) {
+        // Unpadded rows and a power-of-two width: input row r is output row
+        // r, and the indices are a shift and a mask.
+        const int ln = __builtin_ctz(static_cast<unsigned>(n));
+        for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+             idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+            const int64_t r = idx >> ln;
+            const int j = static_cast<int>(idx & (n - 1));
+            const float* xr = a.x + r * k;
+            const float* wr = a.W + static_cast<int64_t>(j) * k;
+            float acc = a.b ? a.b[j] : 0.0f;
+            for (int p = 0; p < k; ++p) acc = lin_step(acc, xr[p], wr[p], p < kplain);
+            a.y[idx] = rt_activate(acc, a.act);
+        }
+        return;
+    }
     const bool narrow_idx = total < (int64_t(1) << 32);
     for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
          idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -669,7 +726,14 @@ hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st) {
         // Registers for as many columns as there are (each column's sum in
         // the same order whatever NMAX is).
         const size_t lds = static_cast<size_t>(a.n) * a.k * sizeof(float);
-        if (a.n == 1)
+        if (a.k == 64 && a.rows_in == a.rows_out && a.rows_valid == a.rows_out && aligned(a.x, 16)) {
+            if (a.n == 1)
+                hipLaunchKernelGGL(k_linear_narrow64<1>, dim3(grid_for(rows, 256, 2)), dim3(256), 0, st, a);
+            else if (a.n <= 4)
+                hipLaunchKernelGGL(k_linear_narrow64<4>, dim3(grid_for(rows, 256, 2)), dim3(256), 0, st, a);
+            else
+                hipLaunchKernelGGL(k_linear_narrow64<16>, dim3(grid_for(rows, 256, 2)), dim3(256), 0, st, a);
+        } else if (a.n == 1)
             hipLaunchKernelGGL(k_linear_narrow<1>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
         else if (a.n <= 4)
             hipLaunchKernelGGL(k_linear_narrow<4>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
