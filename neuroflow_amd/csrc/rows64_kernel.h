@@ -205,6 +205,16 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
     __shared__ uint32_t lds_w[FP8 ? 64 * W_BF16_STRIDE : 1];
     __shared__ v4f lds_sw[16];
     __shared__ v4f lds_b[16];
+    // W_SHARED (the queued INT8 layers): wave 0 loads the weights and forms
+    // the column constants; every wave reads them from LDS after the setup
+    // barrier, so the launch burst carries one 4 KB weight load per block
+    // instead of one per wave (measured at 256 Ki rows, alternating runs on
+    // one device: 22.33-22.39 -> 22.23-22.29 us per layer on one, 23.3-23.4
+    // -> 22.5-22.7 us on another; with four waves, at 32 Ki rows, 6.3 -> 6.8
+    // us, so the static deal keeps the per-wave loads).
+    constexpr bool W_SHARED = QUEUE && !FP8;
+    __shared__ uint32_t lds_wi8[W_SHARED ? 16 * 64 : 1];
+    __shared__ int lds_triv;
     L& my = lds[wid];
 
     // Linear-layout load of one tile: instruction j reads rows 4j .. 4j + 3.
@@ -240,7 +250,7 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
 #pragma unroll
             for (int q = 0; q < 4; ++q) w8[q] = src[q];
         }
-    } else {
+    } else if (!W_SHARED || wid == 0) {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             const uint32_t* src = reinterpret_cast<const uint32_t*>(a.W + (16 * nt + r) * 64 + 16 * g);
@@ -273,7 +283,7 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
             dst[0] = v4u{o[0], o[1], o[2], o[3]};
             dst[1] = v4u{o[4], o[5], o[6], o[7]};
         }
-    } else {
+    } else if (!W_SHARED || wid == 0) {
         // The epilogue constants of column 16 nt + r (row_sum4 reduces the
         // four k-groups' byte sums; K = 64, so the dot covers every k).
 #pragma unroll
@@ -287,8 +297,14 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
             triv[nt] = !__any((mine.c0 != 0) | (mine.c1 != 0) | (mine.c2 != 0));
             if (wid == 0 && g == 0) lds_e[16 * nt + r] = mine;
         }
+        if constexpr (W_SHARED) {
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) lds_wi8[(4 * nt + q) * 64 + lane] = wi8[nt][q];
+            if (lane == 0) lds_triv = (triv[0] ? 1 : 0) | (triv[1] ? 2 : 0) | (triv[2] ? 4 : 0) | (triv[3] ? 8 : 0);
+        }
     }
-    const bool all_triv = triv[0] & triv[1] & triv[2] & triv[3];
     // FIXED: the correctly rounded reciprocal of the scale, and whether the
     // scale is outside the range where the reciprocal codes are certain (then
     // every element takes the exact quotient).
@@ -296,6 +312,16 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
     const bool fixed_exact = FIXED && !(a.scale_A >= 0x1p-120f && a.scale_A <= 0x1p120f);
     if (QUEUE && threadIdx.x == 0) q_next = WPB;
     __syncthreads();
+    if constexpr (W_SHARED) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wi8[nt][q] = lds_wi8[(4 * nt + q) * 64 + lane];
+        const int tb = lds_triv;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) triv[nt] = ((tb >> nt) & 1) != 0;
+    }
+    const bool all_triv = triv[0] & triv[1] & triv[2] & triv[3];
 
     while (tile < ntiles) {
         v4f x[4];
