@@ -400,16 +400,25 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             else dma_step(st_base + Cf::STAGE * sl, nxt, ks - NK);
             if constexpr (k == 0) dma_tables(par, t);
             // Parts 0 and 1 are read first; each later part is read while the
-            // MFMAs of the part two before it run.
+            // MFMAs of the part two before it run.  The scheduling groups pin
+            // that order: left to itself the scheduler moves each read next to
+            // its MFMA (fewer live registers) and every MFMA then waits for a
+            // whole LDS round trip.
             const uint32_t st = st_base + Cf::STAGE * sc;
             v4i xf[4][TI], wf[4][TJ];
             frag_read(st, 0, xf[0], wf[0]);
             frag_read(st, 1, xf[1], wf[1]);
+            __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (TI + TJ), 0);   // DS reads
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
-                if (hh + 2 < 4) frag_read(st, hh + 2, xf[hh + 2], wf[hh + 2]);
+                if (hh + 2 < 4) {
+                    frag_read(st, hh + 2, xf[hh + 2], wf[hh + 2]);
+                    __builtin_amdgcn_sched_group_barrier(0x0100, TI + TJ, 0);
+                }
                 mfma_part(acc, xf[hh], wf[hh]);
+                __builtin_amdgcn_sched_group_barrier(0x0008, TI * TJ, 0);     // MFMA
             }
+            __builtin_amdgcn_sched_barrier(0);
             drain(pacc, par ^ 1, pt, cc, kc);
             sc = sc + 1 == Cf::NS ? 0 : sc + 1;
         });
