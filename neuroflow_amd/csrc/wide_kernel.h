@@ -233,7 +233,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
         const int grp = (lane & 7) ^ (row & 7);
         dvoff[c] = (q < BM / 8 ? row : row - BM) * K + 16 * grp;
     }
-    auto dma_step = [&](uint32_t st, const WideTile& t, int step) {
+    // Loads c0 .. c1 - 1 of the step (all of them by default).
+    auto dma_step = [&](uint32_t st, const WideTile& t, int step, int c0 = 0, int c1 = Cf::NL) {
         const int64_t rows_a = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const int64_t rows_w = t.valid ? (N - t.n0 < BN ? N - t.n0 : BN) : 0;
         const v4u ds_a = wide_desc(a.Aq + t.m0 * K, rows_a * K);
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int q = wid + W * c;
-            wide_dma(q < BM / 8 ? ds_a : ds_w, st + 1024 * q, dvoff[c], ROW * step);
+            if (c >= c0 && c < c1) wide_dma(q < BM / 8 ? ds_a : ds_w, st + 1024 * q, dvoff[c], ROW * step);
         }
     };
     // Tables of tile t into tb[par]: table e is loaded by wave e % W; a wave
@@ -396,9 +397,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             __builtin_amdgcn_s_waitcnt(wide_waitcnt_imm(wide_wait(k, NK, NL, NTAB, STORES, Cf::LEAD)));
             asm volatile("s_barrier" ::: "memory");
             constexpr int ks = k + Cf::LEAD;
-            if constexpr (ks < NK) dma_step(st_base + Cf::STAGE * sl, t, ks);
-            else dma_step(st_base + Cf::STAGE * sl, nxt, ks - NK);
-            if constexpr (k == 0) dma_tables(par, t);
+            // The step's loads go out in groups of NLP, one group ahead of
+            // each K part's MFMAs, then the tables: the same instruction
+            // order as one burst (the waits count the same), spread over the
+            // step.
+            constexpr int NLP = (NL + 2) / 3;
+            auto dma_group = [&](int hh) {
+                if (hh * NLP >= NL) return;
+                if constexpr (ks < NK) dma_step(st_base + Cf::STAGE * sl, t, ks, hh * NLP, hh * NLP + NLP);
+                else dma_step(st_base + Cf::STAGE * sl, nxt, ks - NK, hh * NLP, hh * NLP + NLP);
+                if (k == 0 && hh * NLP + NLP >= NL) dma_tables(par, t);
+            };
             // Parts 0 and 1 are read first; each later part is read while the
             // MFMAs of the part two before it run.  The scheduling groups pin
             // that order: left to itself the scheduler moves each read next to
@@ -411,6 +420,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (TI + TJ), 0);   // DS reads
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
+                dma_group(hh);
                 if (hh + 2 < 4) {
                     frag_read(st, hh + 2, xf[hh + 2], wf[hh + 2]);
                     __builtin_amdgcn_sched_group_barrier(0x0100, TI + TJ, 0);
