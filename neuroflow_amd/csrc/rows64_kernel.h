@@ -286,8 +286,14 @@ __global__ __launch_bounds__(64 * WPB, WPB == 4 ? 3 : 1) void k_rows64(RowsArgs 
     } else if (!W_SHARED || wid == 0) {
         // The epilogue constants of column 16 nt + r (row_sum4 reduces the
         // four k-groups' byte sums; K = 64, so the dot covers every k).
+        // With zp_A = 0, no weight zero points and no caller sum_W (or the
+        // batched formula, which uses sum_W only times zp_A) every constant
+        // is zero whatever the weights: int_epi_consts' c0 is then
+        // 128 S - 128 S, c1 = -2 zp_W and c2 = K zp_W zp_A.  The launch then
+        // skips the byte sums (a branch on kernel arguments, uniform).
+        const bool zero_terms = a.zp_A == 0 && !a.zpW && (!a.sumW || a.formula == F_BATCHED);
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
+        for (int nt = 0; nt < 4 && !zero_terms; ++nt) {
             int32_t ps = 0;
 #pragma unroll
             for (int q = 0; q < 4; ++q) ps = sum_bytes_i8(wi8[nt][q], ps);
