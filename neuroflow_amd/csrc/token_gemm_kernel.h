@@ -116,7 +116,10 @@ __device__ __forceinline__ void token_wave_sync() {
 
 // The product of the 64-row code tile at m0 with every column, by product
 // wave `wid` (0..3): columns 64 wid .. 64 wid + 63 of each 256-column chunk.
-template <int KB, int ACT>
+// SUMS = false when every integer-epilogue term is zero whatever the weights
+// (zp_A = 0, no weight zero points, no caller sum_W or the batched formula):
+// the weight byte sums and the epilogue constants are then skipped.
+template <int KB, int ACT, bool SUMS = true>
 __device__ __forceinline__ void token_tile_gemm(const RowsArgs& a, const uint8_t* codes, const float* lds_s,
                                                 const int32_t* lds_sa, float* strip, uint8_t* ctab, int64_t m0,
                                                 int wid, int lane) {
@@ -163,8 +166,10 @@ __device__ __forceinline__ void token_tile_gemm(const RowsArgs& a, const uint8_t
             for (int ct = 0; ct < 4; ++ct) {
                 const uint8_t* wp = a.W + static_cast<int64_t>(nw0 + 16 * ct + r) * K + 64 * kb + 16 * g;
                 wv[ct] = *reinterpret_cast<const v4i*>(wp);
+                if constexpr (SUMS) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wsum[ct] = sum_bytes_i8(static_cast<uint32_t>(wv[ct][e]), wsum[ct]);
+                    for (int e = 0; e < 4; ++e) wsum[ct] = sum_bytes_i8(static_cast<uint32_t>(wv[ct][e]), wsum[ct]);
+                }
             }
 #pragma unroll
             for (int rt = 0; rt < 4; ++rt)
@@ -177,20 +182,23 @@ __device__ __forceinline__ void token_tile_gemm(const RowsArgs& a, const uint8_t
         }
         // Weight byte sums of column 16 ct + r reduced over the lane groups;
         // lane (r, g) = column 16 g + r takes tile ct = g.
-        int32_t wfull = 0;
+        bool trivial = true;
+        if constexpr (SUMS) {
+            int32_t wfull = 0;
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const int32_t f = row_sum4(wsum[ct]);
-            wfull = (g == ct) ? f : wfull;
+            for (int ct = 0; ct < 4; ++ct) {
+                const int32_t f = row_sum4(wsum[ct]);
+                wfull = (g == ct) ? f : wfull;
+            }
+            const int32_t my_zp = a.zpW ? my_zp0 : 0;
+            const IntEpi mine = int_epi_consts(a.formula, a.K, a.zp_A, my_zp, a.sumW ? my_sg0 : 0,
+                                               a.sumW != nullptr, wfull, wfull);
+            // Wave-uniform: all 64 columns' constants zero, the result is (float)D.
+            trivial = !__any((mine.c0 != 0) | (mine.c1 != 0) | (mine.c2 != 0));
+            if (!trivial) etab[lane] = mine;
         }
-        const int32_t my_zp = a.zpW ? my_zp0 : 0;
-        const IntEpi mine = int_epi_consts(a.formula, a.K, a.zp_A, my_zp, a.sumW ? my_sg0 : 0,
-                                           a.sumW != nullptr, wfull, wfull);
-        // Wave-uniform: all 64 columns' constants zero, the result is (float)D.
-        const bool trivial = !__any((mine.c0 != 0) | (mine.c1 != 0) | (mine.c2 != 0));
         swtab[lane] = my_sw;
         btab[lane] = a.bias ? my_b0 : 0.0f;
-        if (!trivial) etab[lane] = mine;
         token_wave_sync();
         // Epilogue, one 16-row strip at a time through the wave's LDS strip.
 #pragma unroll
@@ -247,6 +255,7 @@ __global__ __launch_bounds__(256, 2) void k_token_gemm(RowsArgs a) {
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
     const int64_t ntiles = (a.M + 63) / 64;
+    const bool zero_terms = a.zp_A == 0 && !a.zpW && (!a.sumW || a.formula == F_BATCHED);
 
     for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
         const int64_t m0 = tile * 64;
@@ -260,7 +269,8 @@ __global__ __launch_bounds__(256, 2) void k_token_gemm(RowsArgs a) {
                 token_quantise_row<J>(a, x[q], m0, 16 * wid + 4 * q + g, r, codes, S::ROW, lds_s, lds_sa);
         }
         __syncthreads();
-        token_tile_gemm<KB, ACT>(a, codes, lds_s, lds_sa, strip, ctab, m0, wid, lane);
+        if (zero_terms) token_tile_gemm<KB, ACT, false>(a, codes, lds_s, lds_sa, strip, ctab, m0, wid, lane);
+        else token_tile_gemm<KB, ACT, true>(a, codes, lds_s, lds_sa, strip, ctab, m0, wid, lane);
         __syncthreads();   // the next tile's quantise overwrites the codes
     }
 }
