@@ -193,6 +193,12 @@ struct nflow_runtime {
     std::map<int, float*> zfill;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // Device copies of the host input and output of nflow_runtime_run,
+    // grown on demand and kept (a device allocation and free per call cost
+    // more than a small batch's whole forward).
+    float* stage_x = nullptr;
+    float* stage_y = nullptr;
+    size_t stage_x_n = 0, stage_y_n = 0;
 
     // Runs on one handle share the tables and the workspace above.  `mu`
     // serialises the host side (table inserts, workspace growth, the INT8
@@ -222,6 +228,8 @@ void free_runtime(nflow_runtime* rt) {
     for (auto& kv : rt->zfill) (void)hipFree(kv.second);
     if (rt->dblock) (void)hipFree(rt->dblock);
     if (rt->ws) (void)hipFree(rt->ws);
+    if (rt->stage_x) (void)hipFree(rt->stage_x);
+    if (rt->stage_y) (void)hipFree(rt->stage_y);
     if (rt->done) (void)hipEventDestroy(rt->done);
     if (sw) (void)hipSetDevice(cur);
     if (rt->ir) nflow_ir_close(rt->ir);
@@ -992,24 +1000,35 @@ int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape,
     if (nx == 0) return NFLOW_OK;
     if (!x || !y) return set_error(NFLOW_INVALID_ARG, "runtime_run: null input/output");
     DeviceGuard g(rt->device);
-    float* dx = nullptr;
-    float* dy = nullptr;
-    if (hipMalloc(reinterpret_cast<void**>(&dx), nx * 4) != hipSuccess) return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
-    if (hipMalloc(reinterpret_cast<void**>(&dy), ny * 4) != hipSuccess) {
-        (void)hipFree(dx);
-        return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
-    }
-    int rc = NFLOW_OK;
     std::unique_lock<std::mutex> lock(rt->mu);
+    // The staging buffers are used only here, under the lock, and every call
+    // ends with the device idle, so growing them never frees a buffer that a
+    // run still reads.
+    auto grow = [](float*& p, size_t& cap, size_t n) {
+        if (cap >= n) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipMalloc(reinterpret_cast<void**>(&p), n * 4) != hipSuccess) {
+            p = nullptr;
+            return false;
+        }
+        cap = n;
+        return true;
+    };
+    if (!grow(rt->stage_x, rt->stage_x_n, nx) || !grow(rt->stage_y, rt->stage_y_n, ny))
+        return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
+    float* dx = rt->stage_x;
+    float* dy = rt->stage_y;
+    int rc = NFLOW_OK;
     if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
     if (!rc) rc = order_run(rt, nullptr);
     if (!rc) rc = mark_run(rt, nullptr, rt->fno2d ? run_device_2d(rt, dx, x_shape, dy, nullptr)
                                                   : run_device(rt, dx, x_shape, dy, nullptr));
     if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess)
         rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
-    if (!rc && hipDeviceSynchronize() != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: device error");
-    (void)hipFree(dx);
-    (void)hipFree(dy);
+    // Always: a failed call may have queued work on the staging buffers.
+    if (hipDeviceSynchronize() != hipSuccess && !rc) rc = set_error(NFLOW_INTERNAL, "runtime_run: device error");
     return rc;
 }
 

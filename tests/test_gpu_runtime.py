@@ -122,6 +122,24 @@ def test_run_device_on_torch_tensors(gpu, tmp_path):
     assert np.array_equal(_bits(yd2.cpu().numpy()), _bits(OF.forward(m, x2)))
 
 
+def test_run_host_buffers_across_batch_sizes(gpu, tmp_path):
+    """run() on host arrays keeps its device copies of the input and output
+    between calls and grows them on demand: a batch of 2, a larger one, a
+    smaller one and the first again each equal the oracle bit for bit."""
+    ncpp = load()
+    case = (8, 256, 1, 1, 32, 12, 4, 1, False, ["tensor"], True)
+    ir, x, m = _model(case)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    rt = ncpp.InferenceRuntime(str(path))
+    rt.enable_int8_gemm()
+    for b, scale in ((2, 1.0), (8, 0.5), (1, 2.0), (2, 1.0)):
+        xb = np.ascontiguousarray(x[:b] * np.float32(scale))
+        y = np.full((b, 256, 1), np.nan, np.float32)
+        rt.run(xb, y)
+        assert np.array_equal(_bits(y), _bits(OF.forward(m, xb))), b
+
+
 def test_infer_and_infer_arrays(gpu, tmp_path):
     ncpp = load()
     case = (3, 32, 1, 2, 16, 6, 3, 1, False, ["tensor"], False)
