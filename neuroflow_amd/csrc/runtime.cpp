@@ -199,6 +199,12 @@ struct nflow_runtime {
     float* stage_x = nullptr;
     float* stage_y = nullptr;
     size_t stage_x_n = 0, stage_y_n = 0;
+    // Pinned host copies for inputs and outputs up to kPinnedStageMax
+    // floats: the caller's (pageable) arrays are copied into them on the host
+    // and moved by DMA, which costs less per small call than a pageable copy.
+    float* pin_x = nullptr;
+    float* pin_y = nullptr;
+    size_t pin_x_n = 0, pin_y_n = 0;
 
     // Runs on one handle share the tables and the workspace above.  `mu`
     // serialises the host side (table inserts, workspace growth, the INT8
@@ -230,6 +236,8 @@ void free_runtime(nflow_runtime* rt) {
     if (rt->ws) (void)hipFree(rt->ws);
     if (rt->stage_x) (void)hipFree(rt->stage_x);
     if (rt->stage_y) (void)hipFree(rt->stage_y);
+    if (rt->pin_x) (void)hipHostFree(rt->pin_x);
+    if (rt->pin_y) (void)hipHostFree(rt->pin_y);
     if (rt->done) (void)hipEventDestroy(rt->done);
     if (sw) (void)hipSetDevice(cur);
     if (rt->ir) nflow_ir_close(rt->ir);
@@ -1018,18 +1026,47 @@ int nflow_runtime_run(nflow_runtime* rt, const float* x, const int64_t* x_shape,
     };
     if (!grow(rt->stage_x, rt->stage_x_n, nx) || !grow(rt->stage_y, rt->stage_y_n, ny))
         return set_error(NFLOW_INTERNAL, "runtime_run: allocation failed");
+    auto grow_pinned = [](float*& p, size_t& cap, size_t n) {
+        if (cap >= n) return true;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        if (hipHostMalloc(reinterpret_cast<void**>(&p), n * 4, hipHostMallocDefault) != hipSuccess) {
+            p = nullptr;
+            return false;
+        }
+        cap = n;
+        return true;
+    };
+    constexpr size_t kPinnedStageMax = size_t(1) << 21;   // floats (8 MiB)
+    const bool pinned = nx <= kPinnedStageMax && ny <= kPinnedStageMax &&
+                        grow_pinned(rt->pin_x, rt->pin_x_n, nx) && grow_pinned(rt->pin_y, rt->pin_y_n, ny);
     float* dx = rt->stage_x;
     float* dy = rt->stage_y;
     int rc = NFLOW_OK;
-    if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
+    if (pinned) {
+        std::memcpy(rt->pin_x, x, nx * 4);
+        if (hipMemcpyAsync(dx, rt->pin_x, nx * 4, hipMemcpyHostToDevice, nullptr) != hipSuccess)
+            rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
+    } else if (hipMemcpy(dx, x, nx * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        rc = set_error(NFLOW_INTERNAL, "runtime_run: input copy failed");
+    }
     if (!rc) rc = order_run(rt, nullptr);
     if (!rc) rc = mark_run(rt, nullptr, rt->fno2d ? run_device_2d(rt, dx, x_shape, dy, nullptr)
                                                   : run_device(rt, dx, x_shape, dy, nullptr));
-    if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess)
+    if (!rc && pinned) {
+        if (hipMemcpyAsync(rt->pin_y, dy, ny * 4, hipMemcpyDeviceToHost, nullptr) != hipSuccess ||
+            hipStreamSynchronize(nullptr) != hipSuccess)
+            rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
+        else
+            std::memcpy(y, rt->pin_y, ny * 4);
+    } else if (!rc && hipMemcpy(y, dy, ny * 4, hipMemcpyDeviceToHost) != hipSuccess) {
         rc = set_error(NFLOW_INTERNAL, "runtime_run: output copy failed");
-    // The output copy returns once the forward queued before it on the null
-    // stream has finished; a failed call may have left work queued on the
-    // staging buffers, so it waits for the device before returning.
+    }
+    // The output copy (and, pinned, the stream synchronise after it) returns
+    // once the forward queued before it on the null stream has finished; a
+    // failed call may have left work queued on the staging buffers, so it
+    // waits for the device before returning.
     if (rc) (void)hipDeviceSynchronize();
     return rc;
 }
