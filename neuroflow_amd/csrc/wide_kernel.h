@@ -327,14 +327,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
             }
         }
     };
-    auto drain = [&](const Acc& acc, int par, const WideTile& t, ColC& cc, auto slc) {
+    // Groups q0 .. q1 - 1 of slice sl (all of it by default).
+    auto drain = [&](const Acc& acc, int par, const WideTile& t, ColC& cc, auto slc, int q0 = 0,
+                     int q1 = Cf::VALS / NK / 4) {
         constexpr int sl = decltype(slc)::value;
         const WideTables& T_ = tb[par];
-        if constexpr (sl == 0) col_consts(T_, cc);
+        if (sl == 0 && q0 == 0) col_consts(T_, cc);
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const auto rs = wide_rsrc(static_cast<float*>(a.C) + t.m0 * N, rows * N * 4);
 #pragma unroll
         for (int qq = 0; qq < PER_STEP; ++qq) {
+            if (qq < q0 || qq >= q1) continue;
             const int vi = 4 * (sl * PER_STEP + qq);
             const int i = vi / (16 * TJ), j = (vi / 16) % TJ, q = (vi % 16) / 4;
             const int col = 32 * TJ * wn + 32 * j + lr;       // within the block tile
@@ -427,9 +430,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
                 }
                 mfma_part(acc, xf[hh], wf[hh]);
                 __builtin_amdgcn_sched_group_barrier(0x0008, TI * TJ, 0);     // MFMA
+                // Half of the slice's stores after part 2's MFMAs, the rest
+                // after part 3's: after the step's last loads either way, so
+                // the waits count the same.
+                if constexpr (PER_STEP >= 2) {
+                    if (hh == 2) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        drain(pacc, par ^ 1, pt, cc, kc, 0, PER_STEP / 2);
+                    }
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
-            drain(pacc, par ^ 1, pt, cc, kc);
+            drain(pacc, par ^ 1, pt, cc, kc, PER_STEP >= 2 ? PER_STEP / 2 : 0, PER_STEP);
             sc = sc + 1 == Cf::NS ? 0 : sc + 1;
         });
     };
