@@ -129,6 +129,33 @@ def test_per_token_layer(gpu, M, N, K, act):
         assert _bits_equal(out, ref)        # dequant + bias (+ relu) is bit-exact
 
 
+@pytest.mark.parametrize("M", [200, 140000])
+def test_symmetric_weights_with_a_mismatched_sum_w(gpu, M):
+    """Zero weight zero points, zp_A = 0 and a caller's sum_W that is not the
+    weights' byte sums, at K = N = 64 (the K = 64 kernel, static deal and tile
+    queue): the batched formula uses sum_W only times zp_A, the per-row (VNNI)
+    formula adds 128 (byte sum - sum_W), and the per-token layer (no zero
+    points at all) takes the same term.  Each equals the oracle bit for bit,
+    so the kernel's choice of which integer terms to form follows the
+    formula, not the weights."""
+    N = K = 64
+    A = WL.normal(21, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 22)          # zps: zeros
+    sumW = (sw + (np.arange(N, dtype=np.int32) % 9) - 4).astype(np.int32)
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), scale_A=0.02, zp_A=0, sum_W_per_row=_cu(sumW))
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 300)), [M - 1]]))
+    rc, ref_b = O.linear_forward_batched(A[rows], q, s, zps, b, 0.02, 0, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(A)))[rows], ref_b)
+    rc, ref_r = O.linear_forward_rows(A[rows], q, s, zps, b, 0.02, 0, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(A)))[rows], ref_r)
+    pt = Q.Int8LinearParams(_cu(q), _cu(s), None, _cu(b), sum_W_per_row=_cu(sumW))
+    out = _host(Q.linear_forward_per_token(pt, _cu(A), "relu"))
+    ref_t, _ = O.layer_per_token_i8(A[rows], q, s, None, b, sumW, 1)
+    assert _bits_equal(out[rows], ref_t)
+
+
 @pytest.mark.parametrize("M,N,K", [(200, 64, 64), (100, 768, 256), (30, 64, 100)])
 @pytest.mark.parametrize("zp_a", [0, 5])
 @pytest.mark.parametrize("with_sum", [False, True])
