@@ -206,6 +206,42 @@ int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64
                                         const int8_t* A_q, const float* scale_A, float* C,
                                         int activation, void* stream);
 
+/* nflow_int8_linear_forward_quantised with 8-bit output: the fp32 result of
+ * that call (y, M x out_features) is quantised per token as
+ * nflow_int8_quantise_per_token quantises it -- scale_C[m] = max_n |y[m][n]| /
+ * 127 (1.0f for an all-zero row), C_q[m][n] = round-half-away(y[m][n] /
+ * scale_C[m]) -- bit for bit, without y ever reaching memory when the layer
+ * is symmetric (zp_W and sum_W_per_row NULL), in_features = 1024 and
+ * out_features a multiple of 256 up to 1024; other layers compute y into a
+ * stream-ordered buffer first.  No single reference function: it is one
+ * step of a chain of per-token layers (the DeepONet branch and trunk MLPs,
+ * cpp/src/fno.cpp:1318-1341, 1364-1386, on the INT8 path of
+ * int8_gemm.cpp:201-470), where the next layer's per-token quantise
+ * (int8_gemm.cpp:507-520 with scale_A = absmax / 127) reads only codes. */
+int nflow_int8_linear_forward_codes(const nflow_int8_linear_params* p, int64_t M, const int8_t* A_q,
+                                    const float* scale_A, int8_t* C_q, float* scale_C, int activation,
+                                    void* stream);
+
+/* A chain of per-token INT8 layers (the MLPs of DeepONet::Forward,
+ * cpp/src/fno.cpp:1318-1341 branch and 1364-1386 trunk, with each Linear on
+ * the per-token INT8 path): h = x; h = nflow_int8_linear_forward_per_token(
+ * layers[l], h, activations[l]) for l = 0 .. n_layers - 1; y = h.  Bit for
+ * bit that sequence.  When every layer is symmetric (zp_W and sum_W_per_row
+ * NULL), layers[0].in_features = 1024 and every hidden width is 1024 (the
+ * last layer's out_features any), the hidden activations stay int8 codes +
+ * row scales (nflow_int8_linear_forward_codes) and only y is fp32; else the
+ * layers run one by one through fp32 buffers.  layers[l + 1].in_features !=
+ * layers[l].out_features -> NFLOW_SHAPE_MISMATCH. */
+int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, const int* activations,
+                                     int n_layers, int64_t M, const float* x, float* y, void* stream);
+
+/* Count of timed-out waits of the 8-bit-output kernel on `stream` since the
+ * last query (it then resets it), after synchronising the stream.  The
+ * kernel's blocks of one row tile wait for each other's row maxima; a wait
+ * that lasts 2 s (blocks that could not run concurrently) gives up, leaves
+ * wrong codes and counts here.  No reference counterpart (a diagnostic). */
+int nflow_debug_chain_faults(void* stream, uint32_t* faults);
+
 /* ---- FP8 E4M3 (cpp/include/neuroflow/fp8_e4m3.h) ---------------------------- */
 
 /* Replaces fp32_array_to_e4m3_bits (fp8_e4m3.h:286-290). */

@@ -70,6 +70,21 @@ __device__ __forceinline__ int32_t quant_i8_token(float a, float s, float inv_s)
     return q;
 }
 
+// Per-token INT8 code of t = a * inv_s for the fast path, and whether it may
+// differ from the reference's.  With s = fl(amax / 127) normal, |a| <= amax
+// and inv_s within 1 ulp of 1 / s (v_rcp_f32), t differs from q = fl(a / s)
+// by at most 2^-22 |t|, and |t| < 127.5.  If the distance of t from
+// r = rint(t) (exact: t and r are within a factor 2) is below
+// 0.5 - 2^-21 |t|, q is closer than 0.5 to r, so round-half-away(q) == r and
+// no clamp is needed.  NaN / Inf elements give a NaN distance and fail.
+__device__ __forceinline__ int32_t quant_i8_near(float a, float inv_s, uint64_t& slow) {
+    const float t = a * inv_s;
+    const float r = rintf(t);
+    const float lim = __builtin_fmaf(fabsf(t), -0x1p-21f, 0.5f);
+    slow |= __builtin_amdgcn_ballot_w64(!(fabsf(t - r) < lim));
+    return static_cast<int32_t>(r);
+}
+
 // Pack four int8 codes (low byte first) into one dword: two v_perm_b32
 // select the low bytes (selector 0x0c zeroes a byte).
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c, int32_t d) {

@@ -108,4 +108,10 @@ bool gemm_pipe_ok(const RowsArgs& a, int out);
 template <int OUT>
 void launch_gemm(const RowsArgs& a, int act, hipStream_t st);
 
+// The 8-bit-output 1024-wide layer (chain.hip): codes + row scales in, the
+// next layer's per-token codes + row scales out.
+struct ChainArgs;
+bool chain_ok(const ChainArgs& a);
+void launch_chain(const ChainArgs& a, int act, hipStream_t st);
+
 }  // namespace nfq

@@ -22,6 +22,7 @@
 #include "common.h"
 #include "launch.h"
 #include "rows_kernel.h"
+#include "chain_kernel.h"
 #include "status.h"
 
 namespace nfq {
@@ -1090,6 +1091,259 @@ int nflow_fp8_linear_forward_quantised(const nflow_fp8_linear_params* p, int64_t
     if (rows_ok(a, IN_CODES)) launch_rows<true, IN_CODES, OUT_EPI>(a, activation, as_stream(stream));
     else launch_generic<true, OUT_EPI>(a, activation, as_stream(stream));
     return check_launch("fp8_linear_forward_quantised");
+}
+
+}  // extern "C"
+
+namespace nfq {
+
+// ---------------------------------------------------------------------------
+// 8-bit-output layers and the per-token layer chain
+// ---------------------------------------------------------------------------
+
+// Row-maxima exchange state of the 8-bit-output kernel, per (device,
+// stream): the published words (zeroed when allocated; every launch tags its
+// words with a new epoch, so a word of an earlier launch never reads as
+// fresh) and a fault word, set by a launch whose wait for the other blocks
+// of a row tile timed out.  Calls on one stream run in order; calls on
+// different streams use different words.  The words grow with the largest M
+// (freed and reallocated in stream order) and live until the process ends.
+struct ChainState {
+    std::mutex mu;
+    uint64_t* part = nullptr;
+    int64_t rows_cap = 0;
+    uint32_t* fault = nullptr;
+};
+
+static ChainState* chain_state(int dev, hipStream_t st) {
+    static std::mutex map_mu;
+    static std::map<std::pair<int, uintptr_t>, std::unique_ptr<ChainState>>* map =
+        new std::map<std::pair<int, uintptr_t>, std::unique_ptr<ChainState>>();
+    std::lock_guard<std::mutex> g(map_mu);
+    auto& e = (*map)[{dev, reinterpret_cast<uintptr_t>(st)}];
+    if (!e) e.reset(new ChainState);
+    return e.get();
+}
+
+// A nonzero tag no earlier launch of this process used (wraps after 2^32 - 1
+// launches).
+static uint32_t next_chain_epoch() {
+    static std::atomic<uint32_t> e{0};
+    uint32_t v;
+    do v = e.fetch_add(1, std::memory_order_relaxed) + 1; while (v == 0);
+    return v;
+}
+
+// A wave waits at most this long (ticks of the 100 MHz clock: 2 s) for the
+// other blocks of its row tile; they run concurrently, so a timeout means
+// they could not be scheduled.
+constexpr int64_t kChainSpinTicks = 200000000;
+constexpr int kChainSlots = 8;   // published words per row, at most (128-column tiles, N <= 1024)
+
+// Words for M rows (and the fault word) in cs, allocated on stream st.
+static int chain_words(ChainState* cs, int64_t M, hipStream_t st) {
+    const int64_t rows = ((M + 127) / 128) * 128;
+    if (!cs->fault) {
+        if (hipMallocAsync(reinterpret_cast<void**>(&cs->fault), 256, st) != hipSuccess) {
+            cs->fault = nullptr;
+            return set_error(NFLOW_INTERNAL, "chain: fault word allocation failed");
+        }
+        if (hipMemsetAsync(cs->fault, 0, 256, st) != hipSuccess) return set_error(NFLOW_INTERNAL, "chain: memset failed");
+    }
+    if (rows > cs->rows_cap) {
+        if (cs->part) (void)hipFreeAsync(cs->part, st);
+        cs->part = nullptr;
+        cs->rows_cap = 0;
+        const int64_t want = std::max<int64_t>(rows, 4096);
+        const size_t bytes = static_cast<size_t>(want) * kChainSlots * sizeof(uint64_t);
+        if (hipMallocAsync(reinterpret_cast<void**>(&cs->part), bytes, st) != hipSuccess) {
+            cs->part = nullptr;
+            return set_error(NFLOW_INTERNAL, "chain: row-maxima allocation failed");
+        }
+        if (hipMemsetAsync(cs->part, 0, bytes, st) != hipSuccess) return set_error(NFLOW_INTERNAL, "chain: memset failed");
+        cs->rows_cap = want;
+    }
+    return NFLOW_OK;
+}
+
+// Whether a layer takes the fused 8-bit-output kernel: symmetric weights
+// (no zero points, no caller sum_W: the integer terms of the formula are 0),
+// K = 1024, N a multiple of 256 up to 1024, 16-byte aligned codes.
+static bool chain_layer_ok(const nflow_int8_linear_params* p) {
+    return !p->zp_W && !p->sum_W_per_row && p->in_features == 1024 && p->out_features >= 256 &&
+           p->out_features <= 1024 && p->out_features % 256 == 0 && aligned(p->W_int8, 16);
+}
+
+// One fused layer on stream st with cs's words (cs locked by the caller).
+static void chain_launch(const nflow_int8_linear_params* p, int64_t M, const uint8_t* Aq, const float* sA,
+                         uint8_t* Cq, float* sC, int act, hipStream_t st, ChainState* cs) {
+    ChainArgs c{};
+    c.Aq = Aq;
+    c.scale_in = sA;
+    c.M = M;
+    c.K = p->in_features;
+    c.N = p->out_features;
+    c.W = reinterpret_cast<const uint8_t*>(p->W_int8);
+    c.sW = p->scale_W;
+    c.bias = p->bias;
+    c.Cq = Cq;
+    c.scale_out = sC;
+    c.part = cs->part;
+    c.fault = cs->fault;
+    c.epoch = next_chain_epoch();
+    c.spin_limit = kChainSpinTicks;
+    launch_chain(c, act, st);
+}
+
+// Codes + row scales -> fp32 (M, N) through the LinearForward formula with
+// zp_A = 0 (the product of nflow_int8_linear_forward_quantised for
+// symmetric layers and for those the tiled kernel forms the byte sums of).
+static void codes_to_f32(const nflow_int8_linear_params* p, int64_t M, const uint8_t* Aq, const float* sA,
+                         float* C, int act, hipStream_t st) {
+    RowsArgs a{};
+    a.Aq = Aq;
+    a.scale_in = sA;
+    a.M = M;
+    a.K = p->in_features;
+    a.N = p->out_features;
+    a.W = reinterpret_cast<const uint8_t*>(p->W_int8);
+    a.sW = p->scale_W;
+    a.zpW = p->zp_W;
+    a.bias = p->bias;
+    a.sumW = p->sum_W_per_row;
+    a.zp_A = 0;
+    a.formula = formula_row(a.K);
+    a.kb_dot = kb_dot_for(a.formula, a.K);
+    a.C = C;
+    if (use_gemm(a)) launch_gemm<OUT_EPI>(a, act, st);
+    else if (rows_ok(a, IN_CODES)) launch_rows<false, IN_CODES, OUT_EPI>(a, act, st);
+    else launch_generic<false, OUT_EPI>(a, act, st);
+}
+
+static int check_layer(const nflow_int8_linear_params* p, int act, const char* what) {
+    if (!p || !p->W_int8 || !p->scale_W) return set_error(NFLOW_INVALID_ARG, std::string(what) + ": null layer parameters");
+    if (p->in_features <= 0 || p->out_features <= 0)
+        return set_error(NFLOW_INVALID_ARG, std::string(what) + ": bad feature dims");
+    if (!valid_act(act)) return set_error(NFLOW_INVALID_ARG, std::string(what) + ": unknown activation");
+    return NFLOW_OK;
+}
+
+}  // namespace nfq
+
+extern "C" {
+
+int nflow_int8_linear_forward_codes(const nflow_int8_linear_params* p, int64_t M, const int8_t* A_q,
+                                    const float* scale_A, int8_t* C_q, float* scale_C, int activation,
+                                    void* stream) {
+    clear_error();
+    if (int rc = check_layer(p, activation, "linear_forward_codes")) return rc;
+    if (!A_q || !scale_A || !C_q || !scale_C) return set_error(NFLOW_INVALID_ARG, "linear_forward_codes: null input/output");
+    if (M <= 0) return NFLOW_OK;
+    hipStream_t st = as_stream(stream);
+    const uint8_t* aq = reinterpret_cast<const uint8_t*>(A_q);
+    uint8_t* cq = reinterpret_cast<uint8_t*>(C_q);
+    if (chain_layer_ok(p) && aligned(aq, 16) && aligned(cq, 4)) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_codes: hipGetDevice failed");
+        ChainState* cs = chain_state(dev, st);
+        std::lock_guard<std::mutex> lock(cs->mu);
+        if (int rc = chain_words(cs, M, st)) return rc;
+        chain_launch(p, M, aq, scale_A, cq, scale_C, activation, st, cs);
+        return check_launch("linear_forward_codes");
+    }
+    // Other layers: the fp32 output into a stream-ordered buffer, then the
+    // per-token quantise (the same bits).
+    float* tmp = nullptr;
+    const size_t bytes = static_cast<size_t>(M) * p->out_features * sizeof(float);
+    if (hipMallocAsync(reinterpret_cast<void**>(&tmp), bytes, st) != hipSuccess)
+        return set_error(NFLOW_INTERNAL, "linear_forward_codes: workspace allocation failed");
+    int rc = nflow_int8_linear_forward_quantised(p, M, A_q, scale_A, tmp, activation, stream);
+    if (rc == NFLOW_OK) {
+        launch_quantise_token<false>(tmp, M, p->out_features, cq, scale_C, nullptr, st);
+        rc = check_launch("linear_forward_codes");
+    }
+    (void)hipFreeAsync(tmp, st);
+    return rc;
+}
+
+int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, const int* activations,
+                                     int n_layers, int64_t M, const float* x, float* y, void* stream) {
+    clear_error();
+    if (!layers || !activations || n_layers <= 0) return set_error(NFLOW_INVALID_ARG, "mlp_forward_per_token: no layers");
+    if (!x || !y) return set_error(NFLOW_INVALID_ARG, "mlp_forward_per_token: null input/output");
+    for (int l = 0; l < n_layers; ++l) {
+        if (int rc = check_layer(&layers[l], activations[l], "mlp_forward_per_token")) return rc;
+        if (l > 0 && layers[l].in_features != layers[l - 1].out_features)
+            return set_error(NFLOW_SHAPE_MISMATCH, "mlp_forward_per_token: layer " + std::to_string(l) +
+                                                       " in_features != the previous layer's out_features");
+    }
+    if (M <= 0) return NFLOW_OK;
+    hipStream_t st = as_stream(stream);
+    if (n_layers == 1) return int8_per_token(&layers[0], M, x, nullptr, y, nullptr, activations[0], nullptr, stream);
+    // Fused: every layer symmetric, every layer but the last on the
+    // 8-bit-output kernel (K = 1024, so every hidden width is 1024).
+    bool fused = aligned(x, 16) && !layers[n_layers - 1].zp_W && !layers[n_layers - 1].sum_W_per_row;
+    for (int l = 0; l < n_layers - 1; ++l) fused = fused && chain_layer_ok(&layers[l]);
+    if (fused) {
+        const size_t codes = static_cast<size_t>(M) * 1024;
+        const size_t codes16 = ((codes + 255) / 256) * 256;
+        const size_t sc = ((static_cast<size_t>(M) * sizeof(float) + 255) / 256) * 256;
+        Scratch ws(2 * codes16 + 2 * sc, st);
+        if (ws.err != hipSuccess) return set_error(NFLOW_INTERNAL, "mlp_forward_per_token: workspace allocation failed");
+        uint8_t* q[2] = {static_cast<uint8_t*>(ws.p), static_cast<uint8_t*>(ws.p) + codes16};
+        float* s[2] = {reinterpret_cast<float*>(q[1] + codes16), reinterpret_cast<float*>(q[1] + codes16 + sc)};
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return set_error(NFLOW_INTERNAL, "mlp_forward_per_token: hipGetDevice failed");
+        ChainState* cs = chain_state(dev, st);
+        std::lock_guard<std::mutex> lock(cs->mu);
+        if (int rc = chain_words(cs, M, st)) return rc;
+        launch_quantise_token<false>(x, M, 1024, q[0], s[0], nullptr, st);
+        int cur = 0;
+        for (int l = 0; l < n_layers - 1; ++l) {
+            chain_launch(&layers[l], M, q[cur], s[cur], q[cur ^ 1], s[cur ^ 1], activations[l], st, cs);
+            cur ^= 1;
+        }
+        codes_to_f32(&layers[n_layers - 1], M, q[cur], s[cur], y, activations[n_layers - 1], st);
+        return check_launch("mlp_forward_per_token");
+    }
+    // Layer by layer through fp32 activations in two stream-ordered buffers.
+    int width = 0;
+    for (int l = 0; l < n_layers - 1; ++l) width = std::max(width, layers[l].out_features);
+    float* h[2] = {nullptr, nullptr};
+    const size_t bytes = static_cast<size_t>(M) * width * sizeof(float);
+    for (auto& b : h)
+        if (hipMallocAsync(reinterpret_cast<void**>(&b), bytes, st) != hipSuccess) {
+            for (auto& f : h)
+                if (f) (void)hipFreeAsync(f, st);
+            return set_error(NFLOW_INTERNAL, "mlp_forward_per_token: workspace allocation failed");
+        }
+    int rc = NFLOW_OK;
+    const float* in = x;
+    for (int l = 0; l < n_layers && rc == NFLOW_OK; ++l) {
+        float* out = l == n_layers - 1 ? y : h[l & 1];
+        rc = int8_per_token(&layers[l], M, in, nullptr, out, nullptr, activations[l], nullptr, stream);
+        in = out;
+    }
+    for (auto& f : h) (void)hipFreeAsync(f, st);
+    return rc;
+}
+
+int nflow_debug_chain_faults(void* stream, uint32_t* faults) {
+    clear_error();
+    if (!faults) return set_error(NFLOW_INVALID_ARG, "debug_chain_faults: null output");
+    *faults = 0;
+    hipStream_t st = as_stream(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(NFLOW_INTERNAL, "debug_chain_faults: hipGetDevice failed");
+    ChainState* cs = chain_state(dev, st);
+    std::lock_guard<std::mutex> lock(cs->mu);
+    if (!cs->fault) return NFLOW_OK;
+    uint32_t v = 0;
+    if (hipMemcpyAsync(&v, cs->fault, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess || hipMemsetAsync(cs->fault, 0, sizeof(uint32_t), st) != hipSuccess)
+        return set_error(NFLOW_INTERNAL, "debug_chain_faults: copy failed");
+    *faults = v;
+    return NFLOW_OK;
 }
 
 }  // extern "C"

@@ -97,21 +97,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, in
         static_cast<int>(left) * row_bytes, 0x00020000);
 }
 
-// Per-token INT8 code of t = a * inv_s for the fast path, and whether it may
-// differ from the reference's.  With s = fl(amax / 127) normal, |a| <= amax
-// and inv_s within 1 ulp of 1 / s (v_rcp_f32), t differs from q = fl(a / s)
-// by at most 2^-22 |t|, and |t| < 127.5.  If the distance of t from
-// r = rint(t) (exact: t and r are within a factor 2) is below
-// 0.5 - 2^-21 |t|, q is closer than 0.5 to r, so round-half-away(q) == r and
-// no clamp is needed.  NaN / Inf elements give a NaN distance and fail.
-__device__ __forceinline__ int32_t quant_i8_near(float a, float inv_s, uint64_t& slow) {
-    const float t = a * inv_s;
-    const float r = rintf(t);
-    const float lim = __builtin_fmaf(fabsf(t), -0x1p-21f, 0.5f);
-    slow |= __builtin_amdgcn_ballot_w64(!(fabsf(t - r) < lim));
-    return static_cast<int32_t>(r);
-}
-
 // Fixed-scale INT8 code (QuantiseActivation with scale_A, zp_A) by the
 // reciprocal, and whether it is certainly the reference's.  inv = fl(1 / s)
 // correctly rounded and, for s in [2^-120, 2^120] (the caller's condition),

@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes as C
 import dataclasses
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -219,6 +219,50 @@ def linear_forward_quantised(p: Int8LinearParams, A_q: torch.Tensor, scale_A: to
                                                          _p(out), _act(activation), _stream()),
           "linear_forward_quantised")
     return out
+
+
+def linear_forward_codes(p: Int8LinearParams, A_q: torch.Tensor, scale_A: torch.Tensor, activation="relu",
+                         out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
+    """linear_forward_quantised followed by the per-token quantise of its
+    output, in one step: (C_q int8 (M, out_features), scale_C float32 (M,)),
+    the next layer's input codes and row scales (nflow_int8_linear_forward_codes)."""
+    _dev(A_q, torch.int8, "A_q")
+    _dev(scale_A, torch.float32, "scale_A")
+    ps = p.c_struct()
+    M = _rows(A_q, p.in_features, "A_q")
+    if out is None:
+        out = (torch.empty(*A_q.shape[:-1], p.out_features, dtype=torch.int8, device=A_q.device),
+               torch.empty(M, dtype=torch.float32, device=A_q.device))
+    C_q, scale_C = out
+    check(_lib.lib().nflow_int8_linear_forward_codes(C.byref(ps), M, _p(A_q), _p(scale_A), _p(C_q),
+                                                     _p(scale_C), _act(activation), _stream()),
+          "linear_forward_codes")
+    return C_q, scale_C
+
+
+def mlp_forward_per_token(layers: Sequence[Int8LinearParams], x: torch.Tensor, activations: Sequence,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """A chain of per-token INT8 layers (DeepONet's branch / trunk MLPs,
+    fno.cpp:1318-1341, 1364-1386): nflow_int8_mlp_forward_per_token."""
+    _dev(x, torch.float32, "x")
+    if len(layers) != len(activations):
+        raise ValueError("one activation per layer")
+    arr = (Int8LinearParamsC * len(layers))(*[L.c_struct() for L in layers])
+    acts = (C.c_int * len(layers))(*[_act(a) for a in activations])
+    M = _rows(x, layers[0].in_features, "x")
+    if out is None:
+        out = torch.empty(*x.shape[:-1], layers[-1].out_features, dtype=torch.float32, device=x.device)
+    check(_lib.lib().nflow_int8_mlp_forward_per_token(arr, acts, len(layers), M, _p(x), _p(out), _stream()),
+          "mlp_forward_per_token")
+    return out
+
+
+def chain_faults() -> int:
+    """Timed-out row-maxima waits of the 8-bit-output kernel on the current
+    stream since the last call (synchronises the stream)."""
+    n = C.c_uint32(0)
+    check(_lib.lib().nflow_debug_chain_faults(_stream(), C.byref(n)), "debug_chain_faults")
+    return int(n.value)
 
 
 # ---- FP8 E4M3 -----------------------------------------------------------------
