@@ -22,24 +22,36 @@
 //    register reduction plus one exchange between the two lane halves, and
 //    four adjacent codes pack into one dword.
 //  - A row's absmax needs all N columns, which N / BN blocks compute.  The
-//    blocks of one row tile run in the same round of the tile deal, on the
-//    same XCD; each publishes its 128 row maxima to global memory as 64-bit
+//    blocks of one row tile run in the same round of the tile deal (on the
+//    same XCD); each publishes its rows' maxima to global memory as 64-bit
 //    words (epoch << 32 | bits of the max), written through to memory (sc1),
 //    and reads the others' two steps later.  The epoch of the launch tells a
 //    fresh word from a stale one, so nothing needs clearing between
-//    launches; a stale word means a block of the row tile is late, and the
-//    wave re-reads (bounded: after spin_limit ticks of the 100 MHz clock it
-//    sets *fault and goes on, so the kernel always ends).
-//  - Drain of tile t during tile t + 1, by step: 0 -> y of row block i = 0
-//    (dequantise + bias + activation, kept in the accumulator registers as
-//    float bits) and its row maxima; 1 -> the same for i = 1, then the
-//    wave's row maxima into LDS; 2 -> the block's maxima (max over the four
-//    column waves) published; 5 -> the row tile's published words DMA'd
-//    into LDS; 6 -> checked, the row scales formed (and stored by the
-//    column-tile-0 block), codes of i = 0 stored; 7 -> codes of i = 1.
+//    launches; a stale word (a block of the row tile running late, or a
+//    line cached before it was written) is re-read from memory past the L2,
+//    bounded: after spin_limit ticks of the 100 MHz clock the wave sets
+//    *fault and goes on, so the kernel always ends.
+//  - The drain of a tile is eight units of 16 values per lane, one per K
+//    step after the step's MFMAs (the whole drain in four of the eight
+//    steps measured 136 us against 107 us without it at 65536 x 1024 x
+//    1024; placed between the MFMA parts, the groups' registers spilled):
+//    A(i, j) forms
+//    y (dequantise + bias + activation, kept in the accumulator registers as
+//    float bits) of row block i (32 rows per wave), column block j, and the
+//    rows' running maxima; B(i, j) quantises it.  Tile t's drain, by step of
+//    tile t + 1 (step 7 of tile t for the first unit):
+//        t.7 A(0,0) | .0 A(0,1), row block 0's wave maxima into LDS
+//        .1 publish block 0, A(1,0) | .2 A(1,1), block 1's maxima into LDS
+//        .3 fetch block 0's words, publish block 1 | .4 row scales of
+//        block 0, B(0,0) | .5 fetch block 1, B(0,1) | .6 row scales of
+//        block 1, B(1,0) | .7 B(1,1)
+//    (128-column tiles have no column block 1: their A(i,1) / B(i,1) are
+//    empty).  The fetch is an LDS DMA of the row block's words; the scales
+//    are read from LDS one step later.
 //  - Every wave issues the same memory instructions in every step (null
 //    ranges where it has nothing to move), so each wait's vmcnt is a
-//    compile-time count, as in k_gemm_wide.
+//    compile-time count, as in k_gemm_wide.  The step's stage loads all go
+//    out at its start, before any store of the drain.
 #pragma once
 
 #include "wide_kernel.h"
@@ -65,8 +77,9 @@ struct ChainArgs {
     int64_t spin_limit;        // wall-clock ticks (100 MHz) a wave waits before giving up
 };
 
-// Cache policy of the published words: written through to memory and read
-// past the L2 (sc1), the coherence point of the CUs of different XCDs.
+// Cache policy of the published words: written through to memory (sc1),
+// where the CUs of every XCD see them.  The words are fetched from the L2
+// (the blocks of a row tile share an XCD); a stale one is re-read past it.
 constexpr int kChainXcdCpol = 16;
 // Code stores: the L2 merges the 8-byte pieces of a row's 128-byte line that
 // the two column waves of a line write.
@@ -81,19 +94,38 @@ struct ChainTables {
     uint32_t spare[256];
 };
 
-// Memory instructions of step k of a tile issued before its stage loads
-// (right after the barrier) and after them (with the step's MFMAs).
+// Per-token INT8 code of a = y / s by the reciprocal inv = 1 / s
+// (correctly rounded), for |a| <= max |row| = 127 s: t = a * inv lies within
+// 2^-22 |t| <= 2^-15 of the correctly rounded quotient q (|t| < 128), so if
+// |t - rint(t)| < 0.5 - 2^-14 then |q - rint(t)| < 0.5 and
+// round_half_away(q) = rint(t), no clamp needed.  Otherwise (near-ties,
+// about one value in 8000, and NaN) `slow` gets the lane's bit and the
+// caller takes the exact path.
+__device__ __forceinline__ int32_t quant_i8_chain(float a, float inv, uint64_t& slow) {
+    const float t = a * inv;
+    const float r = rintf(t);
+    slow |= __builtin_amdgcn_ballot_w64(!(fabsf(t - r) < 0.5f - 0x1p-14f));
+    return static_cast<int32_t>(r);
+}
+
+// The drain's schedule (steps of the next tile) and the memory instructions
+// of step k issued before its stage loads (right after the barrier) and
+// after them (the codes of a B unit).
 template <int TJ>
 struct ChainSteps {
-    static constexpr int NSLOT = 1024 / WideCfg<TJ>::BN;        // published words per row
-    static constexpr int PART_KB = WideCfg<TJ>::BM * NSLOT * 8 / 1024;   // 1 KB DMA loads per tile
-    static constexpr int PUBLISH = 2, FETCH = 5, USE = 6;
-    static constexpr int pre(int k) { return k == PUBLISH ? 1 : k == FETCH ? 1 : k == USE ? 1 : 0; }
-    static constexpr int post(int k) { return k == USE || k == USE + 1 ? 4 * TJ : 0; }
+    static constexpr int NSLOT = 1024 / WideCfg<TJ>::BN;                 // published words per row
+    static constexpr int PART_KB = 32 * NSLOT * 8 / 1024;   // 1 KB DMA loads per 32 rows (one wave row of a row block)
+    static constexpr int PUB0 = 1, FETCH0 = 3, PUB1 = 3, USE0 = 4, FETCH1 = 5, USE1 = 6;
+    static constexpr int pre(int k) {
+        return (k == PUB0) + (k == FETCH0) + (k == PUB1) + (k == USE0) + (k == FETCH1) + (k == USE1);
+    }
+    // B units: (0,0) at step 4, (0,1) at 5, (1,0) at 6, (1,1) at 7; 4 stores each.
+    static constexpr int post(int k) { return (k == 4 || k == 6 || ((k == 5 || k == 7) && TJ == 2)) ? 4 : 0; }
 };
 
 // vmcnt at step k's wait: memory instructions issued after the stage loads
-// of step k (issued in step k - LEAD of this or the previous tile).
+// of step k (issued in step k - LEAD of this or the previous tile), and at
+// the steps that read fetched words, after that fetch.
 template <int TJ>
 constexpr int chain_wait(int k, int nk, int nl, int ntab, int lead) {
     using S = ChainSteps<TJ>;
@@ -103,12 +135,9 @@ constexpr int chain_wait(int k, int nk, int nl, int ntab, int lead) {
         const int j = (k - d + nk) % nk;
         cnt += S::pre(j) + nl + (j == 0 ? ntab : 0) + S::post(j);
     }
-    // Step USE reads what step FETCH's first instruction DMA'd.
-    if (k == S::USE) {
-        const int j = S::FETCH;
-        const int after = nl + (j == 0 ? ntab : 0) + S::post(j);
-        cnt = cnt < after ? cnt : after;
-    }
+    // Step FETCH0's first instruction is the fetch (then the publish).
+    if (k == S::USE0) cnt = cnt < 1 + nl + S::post(S::FETCH0) ? cnt : 1 + nl + S::post(S::FETCH0);
+    if (k == S::USE1) cnt = cnt < nl + S::post(S::FETCH1) ? cnt : nl + S::post(S::FETCH1);
     return cnt;
 }
 
@@ -121,16 +150,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     constexpr int NSLOT = S::NSLOT;
     static_assert(NK == 8 && TI == 2, "schedule of the drain: eight K steps, two row blocks per wave");
     static_assert(Cf::THREADS == kWideThreads, "block size");
-    static_assert(S::PART_KB <= W, "one published-word load per wave at most");
+    static_assert(2 * S::PART_KB <= W, "one published-word load per wave at most");
     using Acc = v16i_w_t[TI][TJ];
     constexpr int NTAB = 1;                       // sw, bias, row scales: one load each, waves 0..2
-    static_assert(chain_wait<TJ>(0, NK, NL, NTAB, Cf::LEAD) < 64 && chain_wait<TJ>(6, NK, NL, NTAB, Cf::LEAD) < 64,
+    static_assert(chain_wait<TJ>(0, NK, NL, NTAB, Cf::LEAD) < 64 && chain_wait<TJ>(1, NK, NL, NTAB, Cf::LEAD) < 64 &&
+                      chain_wait<TJ>(7, NK, NL, NTAB, Cf::LEAD) < 64,
                   "vmcnt field");
     static_assert(Cf::LEAD < NK && Cf::NS == Cf::LEAD + 1, "stage ring");
     __shared__ __attribute__((aligned(16))) uint8_t stages[Cf::NS][Cf::STAGE];
     __shared__ __attribute__((aligned(16))) ChainTables tb[2];
     __shared__ __attribute__((aligned(16))) float pmax[Cf::WN][BM];          // wave row maxima
     __shared__ __attribute__((aligned(16))) uint64_t pub[BM * NSLOT];       // the row tile's published words
+    __shared__ __attribute__((aligned(16))) float srow[2][BM];              // output row scales and reciprocals
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -143,15 +174,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     const int lr = lane & 31, lg = lane >> 5;
 
     // ---- stage loads (as k_gemm_wide) ---------------------------------------
-    int dvoff[NL];
-#pragma unroll
-    for (int c = 0; c < NL; ++c) {
-        const int q = wid + W * c;
-        const int row = 8 * q + (lane >> 3);
-        const int grp = (lane & 7) ^ (row & 7);
-        dvoff[c] = (q < BM / 8 ? row : row - BM) * K + 16 * grp;
-    }
-    auto dma_step = [&](uint32_t st, const WideTile& t, int step, int c0 = 0, int c1 = Cf::NL) {
+    // Lane offset of load c: row 8 q + lane / 8 of the step's rows (A rows,
+    // then W rows), 16-byte group (lane % 8) ^ (row % 8).
+    const int lrow = lane >> 3, lgrp = 16 * ((lane & 7) ^ (lane >> 3));
+    auto dma_step = [&](uint32_t st, const WideTile& t, int step) {
         const int64_t rows_a = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const int64_t rows_w = t.valid ? (N - t.n0 < BN ? N - t.n0 : BN) : 0;
         const v4u ds_a = wide_desc(a.Aq + t.m0 * K, rows_a * K);
@@ -159,7 +185,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
             const int q = wid + W * c;
-            if (c >= c0 && c < c1) wide_dma(q < BM / 8 ? ds_a : ds_w, st + 1024 * q, dvoff[c], ROW * step);
+            wide_dma(q < BM / 8 ? ds_a : ds_w, st + 1024 * q, ((q < BM / 8 ? 8 * q : 8 * q - BM) + lrow) * K + lgrp,
+                     ROW * step);
         }
     };
     // Tables of tile t into tb[par]: wave 0 scale_W, 1 bias, 2 the row
@@ -190,69 +217,62 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
         for (int j = 0; j < TJ; ++j)
             wf[j] = *reinterpret_cast<lds_v4i_ptr>(st + BM * ROW + wide_lds_off(32 * TJ * wn + 32 * j + lr, g));
     };
-    auto mfma_part = [&](Acc& acc, const v4i (&xf)[TI], const v4i (&wf)[TJ]) {
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[j], xf[i], acc[i][j], 0, 0, 0);
-    };
 
     // ---- the drain ---------------------------------------------------------
     // Value v of lane l in tile (i, j): row 64 wm + 32 i + l % 32 of the block
     // tile, column 32 TJ wn + 32 j + 8 (v / 4) + 4 (l / 32) + v % 4.
-    float rmax[TI];
-    float s_row = 1.0f, inv_row = 1.0f;     // this lane's row 64 wm + lane: scale and reciprocal
-    // Phase A of row block i: y in place of the accumulators, row maxima.
-    auto phase_a = [&](Acc& acc, int i, int par) {
+    float rmax[TI];                    // running maxima of the lane's row in row block i
+    // Group g (4 values) of unit A(i, j).
+    auto a_group = [&](Acc& acc, int i, int j, int g, int par, bool live = true) {
+        if (!live) return;
         const ChainTables& T = tb[par];
         const float sa = T.sa[64 * wm + 32 * i + lr];
-        float mx = 0.0f;
+        const int col = 32 * TJ * wn + 32 * j + 8 * g + 4 * lg;
+        const v4f sw = *reinterpret_cast<const v4f*>(T.sw + col);
+        const v4f bb = *reinterpret_cast<const v4f*>(T.bias + col);
+        float mx = (j == 0 && g == 0) ? 0.0f : rmax[i];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = 32 * TJ * wn + 32 * j + 8 * g + 4 * lg;
-                const v4f sw = *reinterpret_cast<const v4f*>(T.sw + col);
-                const v4f bb = *reinterpret_cast<const v4f*>(T.bias + col);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float y = activate<ACT>(dequant_bias(sw[e], sa, static_cast<float>(acc[i][j][4 * g + e]), bb[e]));
-                    mx = fmaxf(mx, fabsf(y));
-                    acc[i][j][4 * g + e] = __builtin_bit_cast(int32_t, y);
-                }
-            }
-        rmax[i] = fmaxf(mx, __shfl_xor(mx, 32));
+        for (int e = 0; e < 4; ++e) {
+            const float y = activate<ACT>(dequant_bias(sw[e], sa, static_cast<float>(acc[i][j][4 * g + e]), bb[e]));
+            mx = fmaxf(mx, fabsf(y));
+            acc[i][j][4 * g + e] = __builtin_bit_cast(int32_t, y);
+        }
+        rmax[i] = mx;
     };
-    // The wave's row maxima into LDS: lane (lg, lr) holds row 32 lg + lr.
-    auto put_wave_max = [&]() { pmax[wn][64 * wm + lane] = lg ? rmax[1] : rmax[0]; };
-    // Publish the block's row maxima (waves of column 0; the others store
-    // into a zero-byte range).
-    auto publish = [&](const WideTile& t) {
+    // The wave's maxima of row block i (both lane halves) into LDS.
+    auto put_wave_max = [&](int i) {
+        const float mx = fmaxf(rmax[i], __shfl_xor(rmax[i], 32));
+        pmax[wn][64 * wm + 32 * i + lr] = mx;
+    };
+    // Publish the block's maxima of row block i (the waves of column 0,
+    // lanes 0..31; the others store into a zero-byte range or past it).
+    auto publish = [&](const WideTile& t, int i) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
-        const bool mine = wn == 0;
-        float mx = pmax[0][64 * wm + lane];
+        const int row = 64 * wm + 32 * i + lr;
+        float mx = pmax[0][row];
 #pragma unroll
-        for (int w2 = 1; w2 < Cf::WN; ++w2) mx = fmaxf(mx, pmax[w2][64 * wm + lane]);
+        for (int w2 = 1; w2 < Cf::WN; ++w2) mx = fmaxf(mx, pmax[w2][row]);
         const v2u_c word = {__builtin_bit_cast(uint32_t, mx), a.epoch};
-        const auto rs = wide_rsrc(mine ? static_cast<void*>(a.part + t.m0 * NSLOT) : nullptr, rows * NSLOT * 8);
-        const int ct = t.n0 / BN;
-        __builtin_amdgcn_raw_buffer_store_b64(word, rs, ((64 * wm + lane) * NSLOT + ct) * 8, 0, kChainXcdCpol);
+        const auto rs = wide_rsrc(wn == 0 ? static_cast<void*>(a.part + t.m0 * NSLOT) : nullptr, rows * NSLOT * 8);
+        // Lane part in the VGPR offset (past the range for lanes 32..63),
+        // the wave-uniform part in the scalar offset.
+        __builtin_amdgcn_raw_buffer_store_b64(word, rs, lg ? 0x40000000 : lr * NSLOT * 8,
+                                              ((64 * wm + 32 * i) * NSLOT + t.n0 / BN) * 8, kChainXcdCpol);
     };
-    // DMA of the row tile's published words into `pub` (waves 0 ..
-    // PART_KB - 1; the others zero bytes into the spare table).
-    auto fetch = [&](const WideTile& t, int par) {
+    // DMA of row block i's published words into `pub`: per wm, 32 rows of
+    // NSLOT words in PART_KB loads of 1 KB (waves 0 .. 2 PART_KB - 1; the
+    // others zero bytes into the spare table).
+    auto fetch = [&](const WideTile& t, int i, int par) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
-        const bool mine = wid < S::PART_KB;
-        const v4u d = wide_desc(mine ? static_cast<const void*>(a.part + t.m0 * NSLOT + 128 * wid) : nullptr,
-                                rows * NSLOT * 8 - 1024 * wid);
-        const uint32_t dst = mine ? wide_lds_addr(pub) + 1024 * wid : wide_lds_addr(tb[par].spare);
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen sc1 lds"
-                     :
-                     : "s"(dst), "v"(16 * lane), "s"(d)
-                     : "memory", "m0");
+        const bool mine = wid < 2 * S::PART_KB;
+        const int fwm = wid / S::PART_KB, half = wid % S::PART_KB;
+        const int row0 = 64 * fwm + 32 * i;
+        const v4u d = wide_desc(mine ? static_cast<const void*>(a.part + (t.m0 + row0) * NSLOT + 128 * half) : nullptr,
+                                (rows - row0) * NSLOT * 8 - 1024 * half);
+        const uint32_t dst = mine ? wide_lds_addr(pub) + row0 * NSLOT * 8 + 1024 * half : wide_lds_addr(tb[par].spare);
+        wide_dma(d, dst, 16 * lane, 0);
     };
-    // Whether word s of row `row` (block-tile index) is this launch's.
+    // Whether the words of global row grow are this launch's.
     auto row_words_fresh = [&](const uint64_t* wds, int64_t grow) {
         bool ok = true;
 #pragma unroll
@@ -260,11 +280,13 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
             if (s2 < n_tiles_n) ok &= static_cast<uint32_t>(wds[s2] >> 32) == a.epoch;
         return ok || grow >= M;
     };
-    // The row scale from the published words of the lane's row 64 wm +
-    // lane: from `pub` (or, with from_global, global memory), re-reading
-    // global memory while any word is stale.
-    auto row_scale = [&](const WideTile& t, bool from_global) {
-        const int row = 64 * wm + lane;
+    // Scale and reciprocal of the lane's row in row block i (into `srow`)
+    // from the published words: from `pub` (or, with from_global, global
+    // memory), re-reading global memory while any word is stale; then the
+    // row scales (column tile 0's waves of column 0, lanes 0..31) into
+    // scale_out.  Each wave reads back only the rows it wrote.
+    auto row_scale = [&](const WideTile& t, int i, bool from_global) {
+        const int row = 64 * wm + 32 * i + lr;
         const int64_t grow = t.m0 + row;
         uint64_t wds[NSLOT];
 #pragma unroll
@@ -288,44 +310,43 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
         for (int s2 = 0; s2 < NSLOT; ++s2)
             if (s2 < n_tiles_n) mb = static_cast<uint32_t>(wds[s2]) > mb ? static_cast<uint32_t>(wds[s2]) : mb;
         const float mx = __builtin_bit_cast(float, mb);
-        s_row = (mx == 0.0f) ? 1.0f : mx / 127.0f;
-        inv_row = 1.0f / s_row;
-        // Column tile 0's wave of column 0 stores the scales.
+        const float so = (mx == 0.0f) ? 1.0f : mx / 127.0f;
+        srow[0][row] = so;
+        srow[1][row] = 1.0f / so;
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const bool mine = wn == 0 && t.n0 == 0;
         const auto rs = wide_rsrc(mine ? static_cast<void*>(a.scale_out + t.m0) : nullptr, rows * 4);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s_row), rs, 4 * row, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, so), rs, lg ? 0x40000000 : 4 * lr,
+                                              4 * (64 * wm + 32 * i), 0);
     };
-    // Phase B of row block i: codes of y / s_out, four per dword.
-    auto phase_b = [&](Acc& acc, int i, const WideTile& t) {
-        const float s = __shfl(s_row, 32 * i + lr);
-        const float inv = __shfl(inv_row, 32 * i + lr);
+    // Group g (4 values) of unit B(i, j): codes of y / s_out, one dword.
+    auto b_group = [&](Acc& acc, int i, int j, int g, const WideTile& t) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const auto rs = wide_rsrc(a.Cq + t.m0 * N, rows * N);
-        const int rbase = (64 * wm + 32 * i + lr) * N + t.n0;
+        const int soff = (64 * wm + 32 * i) * N + t.n0 + 32 * TJ * wn + 32 * j + 8 * g;   // wave-uniform
+        if (!t.valid) {
+            __builtin_amdgcn_raw_buffer_store_b32(0u, rs, 0, 0, 0);
+            return;
+        }
+        float y[4];
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
+        for (int e = 0; e < 4; ++e) {
+            // Through a scalar: clang's __builtin_bit_cast of an ext-vector
+            // element reads the vector's element 0.
+            const int32_t bits = acc[i][j][4 * g + e];
+            y[e] = __builtin_bit_cast(float, bits);
+        }
+        const float inv = srow[1][64 * wm + 32 * i + lr];
+        uint64_t slow = 0;
+        int32_t q[4];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = 32 * TJ * wn + 32 * j + 8 * g + 4 * lg;
-                float y[4];
+        for (int e = 0; e < 4; ++e) q[e] = quant_i8_chain(y[e], inv, slow);
+        if (slow) {
+            const float so = srow[0][64 * wm + 32 * i + lr];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // Through a scalar: clang's __builtin_bit_cast of an
-                    // ext-vector element reads the vector's element 0.
-                    const int32_t bits = acc[i][j][4 * g + e];
-                    y[e] = __builtin_bit_cast(float, bits);
-                }
-                uint64_t slow = 0;
-                int32_t q[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) q[e] = quant_i8_near(y[e], inv, slow);
-                if (slow) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) q[e] = quant_i8_token(y[e], s, inv);
-                }
-                __builtin_amdgcn_raw_buffer_store_b32(pack4(q[0], q[1], q[2], q[3]), rs, rbase + col, 0, kChainCodeCpol);
-            }
+            for (int e = 0; e < 4; ++e) q[e] = quant_i8_token(y[e], so, inv);
+        }
+        __builtin_amdgcn_raw_buffer_store_b32(pack4(q[0], q[1], q[2], q[3]), rs, lr * N + 4 * lg, soff, kChainCodeCpol);
     };
 
     // ---- the step schedule ---------------------------------------------------
@@ -338,10 +359,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
 #pragma unroll
         for (int k = 0; k < Cf::LEAD; ++k) {
             const int j = NK - Cf::LEAD + k;
-            if (S::pre(j) == 1) {
-                if (j == S::FETCH) wide_dma(none, wide_lds_addr(tb[0].spare), 16 * lane, 0);
-                else wide_null_store(none, 4 * lane);
-            }
+            for (int q = 0; q < S::pre(j); ++q) wide_null_store(none, 4 * lane);
             dma_step(st_base + Cf::STAGE * k, cur, k);
             for (int q = 0; q < S::post(j); ++q) wide_null_store(none, 4 * q);
         }
@@ -359,58 +377,85 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
             const int sl = sc + Cf::LEAD >= Cf::NS ? sc + Cf::LEAD - Cf::NS : sc + Cf::LEAD;
             __builtin_amdgcn_s_waitcnt(wide_waitcnt_imm(chain_wait<TJ>(k, NK, NL, NTAB, Cf::LEAD)));
             asm volatile("s_barrier" ::: "memory");
-            // Instructions before the stage loads.
-            if constexpr (k == S::PUBLISH) publish(pt);
-            if constexpr (k == S::FETCH) fetch(pt, par);
-            if constexpr (k == S::USE) row_scale(pt, false);
+            // Before the stage loads.
+            if constexpr (k == S::PUB0) publish(pt, 0);
+            if constexpr (k == S::FETCH0) {
+                fetch(pt, 0, par);
+                publish(pt, 1);
+            }
+            if constexpr (k == S::USE0) row_scale(pt, 0, false);
+            if constexpr (k == S::FETCH1) fetch(pt, 1, par);
+            if constexpr (k == S::USE1) row_scale(pt, 1, false);
+            // The stage loads of step k + LEAD (the next tile's past the end).
             constexpr int ks = k + Cf::LEAD;
-            constexpr int NLP = (NL + 2) / 3;
-            auto dma_group = [&](int hh) {
-                if (hh * NLP >= NL) return;
-                if constexpr (ks < NK) dma_step(st_base + Cf::STAGE * sl, t, ks, hh * NLP, hh * NLP + NLP);
-                else dma_step(st_base + Cf::STAGE * sl, nxt, ks - NK, hh * NLP, hh * NLP + NLP);
-                if (k == 0 && hh * NLP + NLP >= NL) dma_tables(par, t);
+            if constexpr (ks < NK) dma_step(st_base + Cf::STAGE * sl, t, ks);
+            else dma_step(st_base + Cf::STAGE * sl, nxt, ks - NK);
+            if constexpr (k == 0) dma_tables(par, t);
+            // The step's drain unit, a group after each MFMA part.
+            // (Nothing to drain before the first tile: its stores still go
+            // out, on zero-byte ranges, for the counts.)
+            auto unit_group = [&](int g) {
+                if constexpr (k == 0) a_group(pacc, 0, 1, g, par ^ 1, pt.valid);
+                if constexpr (k == 1) a_group(pacc, 1, 0, g, par ^ 1, pt.valid);
+                if constexpr (k == 2) a_group(pacc, 1, 1, g, par ^ 1, pt.valid);
+                if constexpr (k == 4) b_group(pacc, 0, 0, g, pt);
+                if constexpr (k == 5) b_group(pacc, 0, 1, g, pt);
+                if constexpr (k == 6) b_group(pacc, 1, 0, g, pt);
+                if constexpr (k == 7) b_group(pacc, 1, 1, g, pt);
             };
             const uint32_t st = st_base + Cf::STAGE * sc;
             v4i xf[4][TI], wf[4][TJ];
             frag_read(st, 0, xf[0], wf[0]);
-            frag_read(st, 1, xf[1], wf[1]);
-            __builtin_amdgcn_sched_group_barrier(0x0100, 2 * (TI + TJ), 0);
+            __builtin_amdgcn_sched_group_barrier(0x0100, (TI + TJ), 0);
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
-                dma_group(hh);
-                if (hh + 2 < 4) {
-                    frag_read(st, hh + 2, xf[hh + 2], wf[hh + 2]);
+                if (hh + 1 < 4) {
+                    frag_read(st, hh + 1, xf[hh + 1], wf[hh + 1]);
                     __builtin_amdgcn_sched_group_barrier(0x0100, TI + TJ, 0);
                 }
-                mfma_part(acc, xf[hh], wf[hh]);
-                __builtin_amdgcn_sched_group_barrier(0x0008, TI * TJ, 0);
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[hh][j], xf[hh][i], acc[i][j], 0, 0, 0);
+                // The group's VALU work between the part's MFMAs.
+#pragma unroll
+                for (int q = 0; q < TI * TJ; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x0002, 8, 0);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
-            // Instructions after the stage loads.
-            if constexpr (k == 0) phase_a(pacc, 0, par ^ 1);
-            if constexpr (k == 1) {
-                phase_a(pacc, 1, par ^ 1);
-                put_wave_max();
-            }
-            if constexpr (k == S::USE) phase_b(pacc, 0, pt);
-            if constexpr (k == S::USE + 1) phase_b(pacc, 1, pt);
+            if constexpr (TJ == 2 || (k != 0 && k != 2 && k != 5 && k != 7))
+                for (int g = 0; g < 4; ++g) unit_group(g);
+            // This tile's first unit, once its accumulators are final.
+            if constexpr (k == NK - 1)
+                for (int g = 0; g < 4; ++g) a_group(acc, 0, 0, g, par);
+            if constexpr (k == 0 || k == 2) put_wave_max(k == 0 ? 0 : 1);
             sc = sc + 1 == Cf::NS ? 0 : sc + 1;
         });
     };
-    // The last tile: the whole drain in sequence.
+    // The last tile: the rest of its drain in sequence (A(0,0) ran in its
+    // step 7), reading the others' words from global memory.
     auto final_drain = [&](Acc& acc, int par, const WideTile& t) {
         __builtin_amdgcn_s_waitcnt(0x070);
         asm volatile("s_barrier" ::: "memory");
-        phase_a(acc, 0, par);
-        phase_a(acc, 1, par);
-        put_wave_max();
+        if constexpr (TJ == 2)
+            for (int g = 0; g < 4; ++g) a_group(acc, 0, 1, g, par);
+        put_wave_max(0);
+        for (int g = 0; g < 4; ++g) a_group(acc, 1, 0, g, par);
+        if constexpr (TJ == 2)
+            for (int g = 0; g < 4; ++g) a_group(acc, 1, 1, g, par);
+        put_wave_max(1);
         __syncthreads();
-        publish(t);
-        // Every wave reads the row tile's words from global memory.
-        row_scale(t, true);
-        phase_b(acc, 0, t);
-        phase_b(acc, 1, t);
+        publish(t, 0);
+        publish(t, 1);
+        row_scale(t, 0, true);
+        for (int j = 0; j < TJ; ++j)
+            for (int g = 0; g < 4; ++g) b_group(acc, 0, j, g, t);
+        row_scale(t, 1, true);
+        for (int j = 0; j < TJ; ++j)
+            for (int g = 0; g < 4; ++g) b_group(acc, 1, j, g, t);
     };
 
 #pragma unroll

@@ -451,12 +451,15 @@ struct WsEntry {
     size_t cap = 0;
 };
 
-static WsEntry* ws_entry(int dev, hipStream_t st) {
+// Slot 0 is a call's own workspace; slot 1 holds the fp32 activations
+// between the layers of nflow_int8_mlp_forward_per_token, whose per-layer
+// calls take slot 0 meanwhile.
+static WsEntry* ws_entry(int dev, hipStream_t st, int slot) {
     static std::mutex map_mu;
     static std::map<std::pair<int, uintptr_t>, std::unique_ptr<WsEntry>>* map =
         new std::map<std::pair<int, uintptr_t>, std::unique_ptr<WsEntry>>();
     std::lock_guard<std::mutex> g(map_mu);
-    auto& e = (*map)[{dev, reinterpret_cast<uintptr_t>(st)}];
+    auto& e = (*map)[{dev * 2 + slot, reinterpret_cast<uintptr_t>(st)}];
     if (!e) e.reset(new WsEntry);
     return e.get();
 }
@@ -467,7 +470,7 @@ struct Scratch {
     hipError_t err = hipSuccess;
     bool owned = false;                    // per-call allocation (freed here)
     std::unique_lock<std::mutex> lock;
-    Scratch(size_t bytes, hipStream_t s) : st(s) {
+    Scratch(size_t bytes, hipStream_t s, int slot = 0) : st(s) {
         bytes = std::max<size_t>(bytes, 256);
         int dev = 0;
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -477,7 +480,7 @@ struct Scratch {
             owned = err == hipSuccess;
             return;
         }
-        WsEntry* e = ws_entry(dev, s);
+        WsEntry* e = ws_entry(dev, s, slot);
         lock = std::unique_lock<std::mutex>(e->mu);
         if (bytes > e->cap) {
             if (e->p) (void)hipFreeAsync(e->p, s);
@@ -1281,8 +1284,13 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
     hipStream_t st = as_stream(stream);
     if (n_layers == 1) return int8_per_token(&layers[0], M, x, nullptr, y, nullptr, activations[0], nullptr, stream);
     // Fused: every layer symmetric, every layer but the last on the
-    // 8-bit-output kernel (K = 1024, so every hidden width is 1024).
-    bool fused = aligned(x, 16) && !layers[n_layers - 1].zp_W && !layers[n_layers - 1].sum_W_per_row;
+    // 8-bit-output kernel (K = 1024, so every hidden width is 1024), and
+    // rows enough for two 128 x 256 tiles per CU: with one tile per CU the
+    // 8-bit-output kernel's last row-maxima exchange is not overlapped
+    // (measured at 4096 rows, K = N = 1024: 17.9 us against 11.2 us for the
+    // fp32-output product, more than the quantise launch it saves).
+    bool fused = aligned(x, 16) && !layers[n_layers - 1].zp_W && !layers[n_layers - 1].sum_W_per_row &&
+                 ((M + 127) / 128) * 4 >= 2 * static_cast<int64_t>(num_cus());
     for (int l = 0; l < n_layers - 1; ++l) fused = fused && chain_layer_ok(&layers[l]);
     if (fused) {
         const size_t codes = static_cast<size_t>(M) * 1024;
@@ -1306,17 +1314,14 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
         codes_to_f32(&layers[n_layers - 1], M, q[cur], s[cur], y, activations[n_layers - 1], st);
         return check_launch("mlp_forward_per_token");
     }
-    // Layer by layer through fp32 activations in two stream-ordered buffers.
+    // Layer by layer through fp32 activations in two buffers of the stream's
+    // second workspace slot (each layer's own workspace is slot 0).
     int width = 0;
     for (int l = 0; l < n_layers - 1; ++l) width = std::max(width, layers[l].out_features);
-    float* h[2] = {nullptr, nullptr};
-    const size_t bytes = static_cast<size_t>(M) * width * sizeof(float);
-    for (auto& b : h)
-        if (hipMallocAsync(reinterpret_cast<void**>(&b), bytes, st) != hipSuccess) {
-            for (auto& f : h)
-                if (f) (void)hipFreeAsync(f, st);
-            return set_error(NFLOW_INTERNAL, "mlp_forward_per_token: workspace allocation failed");
-        }
+    const size_t hb = ((static_cast<size_t>(M) * width * sizeof(float) + 255) / 256) * 256;
+    Scratch hs(2 * hb, st, 1);
+    if (hs.err != hipSuccess) return set_error(NFLOW_INTERNAL, "mlp_forward_per_token: workspace allocation failed");
+    float* h[2] = {static_cast<float*>(hs.p), reinterpret_cast<float*>(static_cast<uint8_t*>(hs.p) + hb)};
     int rc = NFLOW_OK;
     const float* in = x;
     for (int l = 0; l < n_layers && rc == NFLOW_OK; ++l) {
@@ -1324,7 +1329,6 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
         rc = int8_per_token(&layers[l], M, in, nullptr, out, nullptr, activations[l], nullptr, stream);
         in = out;
     }
-    for (auto& f : h) (void)hipFreeAsync(f, st);
     return rc;
 }
 
