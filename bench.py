@@ -140,6 +140,64 @@ def time_gemm_only(wl, layers, sets, stream, reps):
     return us, gemm_bytes, 2 * M * N * K
 
 
+def chained(wl):
+    """Whether the workload's step is one per-token layer chain (each layer
+    reading the previous one's output): the DeepONet MLPs, run through
+    nflow_int8_mlp_forward_per_token, whose hidden activations stay int8
+    codes + row scales."""
+    return all(L.fmt == "int8" and L.src is None for L in wl.layers) and wl.name.startswith("C5")
+
+
+def chain_fused(wl):
+    """Whether the library takes the 8-bit-output kernel for the chain: its
+    condition in nflow_int8_mlp_forward_per_token (K = 1024 hidden layers,
+    rows enough for two 128 x 256 tiles per CU)."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return (chained(wl) and all(L.W.shape[1] == 1024 for L in wl.layers)
+            and all(L.W.shape[0] == 1024 for L in wl.layers[:-1]) and (wl.M + 127) // 128 * 4 >= 2 * cus)
+
+
+def time_codes_only(wl, layers, stream, reps):
+    """Average duration of the 8-bit-output kernel alone (layer 0: codes and
+    row scales in, the next layer's codes and row scales out), on per-token
+    codes of the workload's input prepared outside the timed region, over 4
+    rotating buffer sets."""
+    import ctypes as C
+
+    import torch
+    from neuroflow_amd import _lib
+    from neuroflow_amd import quant as Q
+    obj, _, L = layers[0]
+    M, N, K = wl.M, L.W.shape[0], L.W.shape[1]
+    x = torch.from_numpy(wl.x).to("cuda")
+    q0, s0, _ = Q.quantise_per_token(x)
+    del x
+    ins = [(q0, s0)] + [(q0.clone(), s0.clone()) for _ in range(3)]
+    outs = [(torch.empty(M, N, dtype=torch.int8, device="cuda"), torch.empty(M, device="cuda")) for _ in ins]
+    ps = obj.token_params.c_struct()
+    fn = _lib.lib().nflow_int8_linear_forward_codes
+    act = {"none": 0, "relu": 1, "gelu": 2}[L.act]
+    sptr = stream.cuda_stream
+
+    def launch(i):
+        (q, sc), (cq, cs) = ins[i % 4], outs[i % 4]
+        _lib.check(fn(C.byref(ps), M, q.data_ptr(), sc.data_ptr(), cq.data_ptr(), cs.data_ptr(), act, sptr),
+                   "linear_forward_codes")
+
+    for i in range(3):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    return us, M * K + M * N + 8 * M + N * K + 8 * N, 2 * M * N * K
+
+
 def build_layers(wl, dev):
     from neuroflow_amd import quant as Q
     layers = []
@@ -220,6 +278,8 @@ def cpu_baseline(wl, layers, legs=("token",), budget_log2=32):
 
 def _kernel_of(wl):
     N0, K0 = wl.layers[0].W.shape
+    if chain_fused(wl):
+        return "nfq::k_chain_wide"    # 8-bit-output layers after one per-token quantise launch
     if K0 == 64 and N0 == 64:
         return "nfq::k_rows64"
     if (wl.layers[0].fmt == "int8" and all(l.W.shape[1] in (128, 256, 512) and l.W.shape[0] % 64 == 0
@@ -258,6 +318,29 @@ def check_timed_step(wl, layers, bufs):
                    "exact-product oracle"}
 
 
+def check_chain_step(wl, layers, bufs):
+    """Oracle parity of a chained step's output (sampled rows): the oracle's
+    per-token layers applied in sequence to the step's input rows."""
+    import torch
+    from oracle import parity as P
+
+    x = bufs["in"][0]
+    y = bufs["out"][-1]
+    N, K = wl.layers[0].W.shape
+    rows = P.sample_rows(wl.M, K, N)
+    idx = torch.from_numpy(rows).to(x.device)
+    h = x.index_select(0, idx).cpu().numpy()
+    for obj, _, L in layers:
+        h, _ = P.layer_ref(L.fmt, obj.W_q, obj.scale_W, getattr(obj, "sum_W", None), L.bias, h, L.act)
+    got = y.index_select(0, idx).cpu().numpy()
+    r = P.compare(got, h, wl.layers[-1].fmt, "gelu" if any(L.act == "gelu" for L in wl.layers) else "none")
+    return {"ok": r["ok"], "layers": len(layers), "rows_per_layer": [r["rows"]] * len(layers),
+            "bit_exact_frac_min": round(r["bit_exact_frac"], 6), "max_abs_diff": r["max_abs"],
+            "checked": "the chain's output against the oracle's per-token layers in sequence",
+            "bar": "INT8: bit-exact without GELU, 1e-5 rel / 1e-6 abs with GELU; FP8: 1e-5 / 1e-6 of the "
+                   "exact-product oracle"}
+
+
 def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, graph=False):
     """Times `steps` steps of workload `name` (after `warmup`) and returns its
     measurement record."""
@@ -275,22 +358,38 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
 
     # Buffer sets (the inputs and one output per layer), rotated across steps
     # so that a step's input is not resident in the 256 MB last-level cache.
-    set_bytes = sum(x.nbytes for x in wl.inputs) + sum(4 * M * L.W.shape[0] for L in wl.layers)
+    # A chained workload (one call per step) keeps only the last output.
+    chain = chained(wl)
+    out_layers = wl.layers[-1:] if chain else wl.layers
+    set_bytes = sum(x.nbytes for x in wl.inputs) + sum(4 * M * L.W.shape[0] for L in out_layers)
     n_sets = args.sets or max(2, min(8, -(-1_100_000_000 // set_bytes)))
     host_in = [torch.from_numpy(x) for x in wl.inputs]
     sets = []
     for _ in range(n_sets):
         sets.append({"in": [h.to(dev) for h in host_in],
-                     "out": [torch.empty(M, L.W.shape[0], dtype=torch.float32, device=dev) for L in wl.layers]})
+                     "out": [torch.empty(M, L.W.shape[0], dtype=torch.float32, device=dev) for L in out_layers]})
     torch.cuda.synchronize()
     srcs = [wl.source(l) for l in range(len(layers))]
 
-    def step(i, sp=sptr):
-        b = sets[i % n_sets]
-        for l, (_, run, _) in enumerate(layers):
-            kind, k = srcs[l]
-            src = b["in"][k] if kind == "input" else b["out"][k]
-            run(src.data_ptr(), b["out"][l].data_ptr(), M, sp)
+    if chain:
+        import ctypes as C
+        from neuroflow_amd import _lib
+        from neuroflow_amd._lib import Int8LinearParamsC
+        chain_ps = (Int8LinearParamsC * len(layers))(*[obj.token_params.c_struct() for obj, _, _ in layers])
+        chain_acts = (C.c_int * len(layers))(*[{"none": 0, "relu": 1, "gelu": 2}[L.act] for _, _, L in layers])
+        chain_fn = _lib.lib().nflow_int8_mlp_forward_per_token
+
+        def step(i, sp=sptr):
+            b = sets[i % n_sets]
+            _lib.check(chain_fn(chain_ps, chain_acts, len(layers), M, b["in"][0].data_ptr(),
+                                b["out"][-1].data_ptr(), sp), "mlp_forward_per_token")
+    else:
+        def step(i, sp=sptr):
+            b = sets[i % n_sets]
+            for l, (_, run, _) in enumerate(layers):
+                kind, k = srcs[l]
+                src = b["in"][k] if kind == "input" else b["out"][k]
+                run(src.data_ptr(), b["out"][l].data_ptr(), M, sp)
 
     # Device pre-warm: the same steps for at least `args.prewarm_ms` of wall
     # time, in batches that double in size (a synchronize after each), ahead of
@@ -358,7 +457,8 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
     # Parity of the timed step: the last timed step wrote set (steps - 1) % n_sets.
     parity = None
     if args.check:
-        parity = check_timed_step(wl, layers, sets[(steps - 1) % n_sets])
+        bufs = sets[(steps - 1) % n_sets]
+        parity = check_chain_step(wl, layers, bufs) if chain else check_timed_step(wl, layers, bufs)
 
     bytes_step = sum(wl.bytes_per_layer(l) for l in range(len(layers)))
     ops_step = sum(wl.ops_per_layer(l) for l in range(len(layers)))
@@ -382,7 +482,19 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
                  "bytes_per_launch": bytes_step // len(layers),
                  "ops_per_launch": ops_step // len(layers),
                  "tops": round(tops, 2), "gbs": round(gbs, 1)})
-    if kernel in ("nfq::k_gemm_pipe", "nfq::k_gemm_wide"):
+    if kernel == "nfq::k_chain_wide":
+        # The hidden layers are one launch each (codes in, codes out) after
+        # the first layer's quantise; the roofline is that kernel's own,
+        # timed alone on layer 0's shape.
+        g_us, g_bytes, g_ops = time_codes_only(wl, layers, stream, max(20, steps))
+        g_gbs, g_tops = g_bytes / (g_us * 1e-6) / 1e9, g_ops / (g_us * 1e-6) / 1e12
+        roof.update({"layer_avg_us": round(kernel_us, 3), "kernel_avg_us": round(g_us, 3),
+                     "bytes_per_launch": g_bytes, "ops_per_launch": g_ops,
+                     "tops": round(g_tops, 2), "gbs": round(g_gbs, 1),
+                     "achieved": round(g_tops, 2), "frac": round(g_tops / MFMA_PEAK_TOPS[fmt], 4),
+                     "layer_level_tops": round(tops, 2),
+                     "layer_level_frac": round(tops / MFMA_PEAK_TOPS[fmt], 4)})
+    elif kernel in ("nfq::k_gemm_pipe", "nfq::k_gemm_wide"):
         # The layer is two launches (quantise, then the GEMM); the roofline
         # is the GEMM kernel's own, timed alone on layer 0's shape.
         g_us, g_bytes, g_ops = time_gemm_only(wl, layers, sets, stream, max(20, steps))
@@ -399,9 +511,9 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
     copy = None
     if copy_calib:
         L0 = wl.layers[0]
-        n_out = M * min(L0.W.shape)          # within both the input and the output
         srcs_c = [s_["in"][0] for s_ in sets]
         dsts = [s_["out"][0] for s_ in sets]
+        n_out = min(M * min(L0.W.shape), dsts[0].numel())   # within both the input and the output
         # torch.neg is one elementwise kernel that reads and writes each
         # float once (a same-dtype copy_ would go to the runtime's blit).
         for i in range(3):
