@@ -14,8 +14,13 @@
  * name starts with nflow_host_.  Kernels are enqueued on `stream` (a
  * hipStream_t; NULL = the default stream) and the call returns without
  * synchronising; results are ready once the stream has been synchronised.
- * Calls on one stream execute in order; the library keeps no state between
- * calls except a cached device-property lookup.
+ * Calls on one stream execute in order.  State kept between calls: device
+ * properties and kernel-path flags (process-wide); per (device, stream), the
+ * workspace buffers of the entry points that stage codes between launches and
+ * the row-maxima words of the 8-bit-output layer, kept at the largest size
+ * asked for until nflow_release_stream_workspace or the end of the process;
+ * per device, the static scratch of
+ * nflow_int8_linear_forward_per_token_noalloc.
  *
  * Numerics (the reference's x86 build is the specification):
  *   - activation codes: clamp(int32(roundf(a / scale)) + zp, -128, 127) with a
@@ -168,10 +173,9 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
 #define NFLOW_NOALLOC_SCRATCH_BYTES ((size_t)72 << 20)
 
 /* nflow_int8_linear_forward_per_token that allocates nothing.  No
- * counterpart in the reference (whose per-token path allocates a
- * std::vector per call, int8_gemm.cpp:247): it is for callers that cannot
- * allocate -- code under HIP graph capture, tight serving loops, harnesses
- * that forbid hipMalloc.  Same arguments and results, bit for bit.  The
+ * counterpart in the reference: it is for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments and results, bit for bit.  The
  * shapes the one-launch kernels do not take (e.g. K = 1024: per-token
  * quantise into codes, then the tiled GEMM) keep their codes, scales and
  * byte sums in a static device array of NFLOW_NOALLOC_SCRATCH_BYTES held by
@@ -180,8 +184,11 @@ int nflow_int8_linear_forward_per_token(const nflow_int8_linear_params* p, int64
  * (scales, unless scale_A_out is given), + 4M (row code sums, with zero
  * points), + 4N (weight-row sums, with a caller's sum_W); a call needing more
  * than the array returns NFLOW_INVALID_ARG before anything is launched.
- * Every call on one GPU shares that array: calls that can overlap on the
- * device (different streams, not ordered by the caller) race. */
+ * Every call on one GPU shares that array and keeps nothing in it between
+ * calls.  Host threads are safe when their calls share a stream: a
+ * per-device lock is held from the array's lookup until the call's last
+ * launch, so their launches do not interleave.  Calls on different streams
+ * that the caller does not order race on the device. */
 int nflow_int8_linear_forward_per_token_noalloc(const nflow_int8_linear_params* p, int64_t M,
                                                 const float* A, float* C, float* scale_A_out,
                                                 int activation, void* stream);
@@ -234,6 +241,15 @@ int nflow_int8_linear_forward_codes(const nflow_int8_linear_params* p, int64_t M
  * layers[l].out_features -> NFLOW_SHAPE_MISMATCH. */
 int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, const int* activations,
                                      int n_layers, int64_t M, const float* x, float* y, void* stream);
+
+/* Frees, in stream order, the buffers the library keeps for `stream` on
+ * the current device (the workspaces of the per-token entry points and of
+ * nflow_int8_mlp_forward_per_token, the 8-bit-output layer's row-maxima
+ * words); the next call on the stream allocates anew.  For callers that
+ * create and destroy streams: call it before hipStreamDestroy, or a later
+ * stream with the same handle reuses the buffers.  No reference
+ * counterpart (the reference allocates per call, int8_gemm.cpp:247, 539). */
+int nflow_release_stream_workspace(void* stream);
 
 /* Count of timed-out waits of the 8-bit-output kernel on `stream` since the
  * last query (it then resets it), after synchronising the stream.  The

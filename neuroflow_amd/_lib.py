@@ -93,6 +93,7 @@ SIGNATURES = {
     "nflow_int8_linear_forward_codes": [_P8, _i64, _vp, _vp, _vp, _vp, _i32, _vp],
     "nflow_int8_mlp_forward_per_token": [_P8, C.POINTER(C.c_int), _i32, _i64, _vp, _vp, _vp],
     "nflow_debug_chain_faults": [_vp, C.POINTER(C.c_uint32)],
+    "nflow_release_stream_workspace": [_vp],
     "nflow_fp8_e4m3_to_bits": [_vp, _vp, _i64, _vp],
     "nflow_fp8_e4m3_from_bits": [_vp, _vp, _i64, _vp],
     "nflow_fp8_e4m3_fake_quant": [_vp, _f32, _vp, _i64, _vp],

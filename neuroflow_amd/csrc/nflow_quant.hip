@@ -694,15 +694,22 @@ constexpr size_t kNoAllocScratchBytes = NFLOW_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 // The current device's address of `scratch`, looked up on the first call
-// that needs it on that device and kept per device.
-static int noalloc_scratch_address(void** out) {
-    constexpr int kMaxDevices = 64;
+// that needs it on that device and kept per device, and that device's lock
+// on it: a call holds the lock from the lookup until its product is
+// launched, so host threads whose calls share one stream cannot interleave
+// their quantise and product launches on the one array (launches on
+// different streams still run concurrently on the device and race).
+constexpr int kMaxDevices = 64;
+static std::mutex noalloc_mu[kMaxDevices];
+
+static int noalloc_scratch_address(void** out, std::unique_lock<std::mutex>* hold) {
     static std::mutex mu;
     static void* addr[kMaxDevices] = {};
     int dev = 0;
     const hipError_t ed = hipGetDevice(&dev);
     if (ed != hipSuccess) return set_error(NFLOW_INTERNAL, std::string("noalloc scratch: hipGetDevice: ") + hipGetErrorString(ed));
     if (dev < 0 || dev >= kMaxDevices) return set_error(NFLOW_INTERNAL, "noalloc scratch: device index out of range");
+    *hold = std::unique_lock<std::mutex>(noalloc_mu[dev]);
     std::lock_guard<std::mutex> lock(mu);
     if (!addr[dev]) {
         void* ptr = nullptr;
@@ -794,7 +801,8 @@ static int int8_per_token(const nflow_int8_linear_params* p, int64_t M, const fl
                                                     std::to_string(need) + " bytes of scratch, more than the " +
                                                     std::to_string(fixed->cap) + " the library holds (split the rows)");
         void* base = nullptr;
-        if (int rc = noalloc_scratch_address(&base)) return rc;
+        std::unique_lock<std::mutex> hold;   // until the product is launched (end of scope)
+        if (int rc = noalloc_scratch_address(&base, &hold)) return rc;
         uint8_t* q = static_cast<uint8_t*>(base);
         float* sc = scale_A_out ? scale_A_out : reinterpret_cast<float*>(q + codes16);
         int32_t* sums0 = reinterpret_cast<int32_t*>(q + codes16 + (scale_A_out ? 0 : static_cast<size_t>(M) * sizeof(float)));
@@ -1330,6 +1338,28 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
         in = out;
     }
     return rc;
+}
+
+int nflow_release_stream_workspace(void* stream) {
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return set_error(NFLOW_INTERNAL, "release_stream_workspace: hipGetDevice failed");
+    for (int slot = 0; slot < 2; ++slot) {
+        WsEntry* e = ws_entry(dev, st, slot);
+        std::lock_guard<std::mutex> lock(e->mu);
+        if (e->p) (void)hipFreeAsync(e->p, st);
+        e->p = nullptr;
+        e->cap = 0;
+    }
+    ChainState* cs = chain_state(dev, st);
+    std::lock_guard<std::mutex> lock(cs->mu);
+    if (cs->part) (void)hipFreeAsync(cs->part, st);
+    if (cs->fault) (void)hipFreeAsync(cs->fault, st);
+    cs->part = nullptr;
+    cs->fault = nullptr;
+    cs->rows_cap = 0;
+    return check_launch("release_stream_workspace");
 }
 
 int nflow_debug_chain_faults(void* stream, uint32_t* faults) {

@@ -17,12 +17,17 @@ bool rows64_ok(const RowsArgs& a) {
 template <bool FP8, int ACT, bool RES, int XQ, bool FIXED = false>
 static void launch_rows64_act(const RowsArgs& a, hipStream_t st) {
     // With at least two tiles per wave at one 16-wave block per CU: the
-    // tile queue (one block per CU, its waves taking tiles as they go).
+    // tile queue (one block per CU, its waves taking tiles as they go).  Not
+    // for the FNO layer with a residual and the per-position x2 fake-quant:
+    // in a 1024-thread block (128 VGPRs per lane) that form spills (64 bytes
+    // per lane for INT8, 20 for FP8), so it keeps the 4-wave blocks.
     const int64_t ntiles = (a.M + 15) / 16;
-    if (ntiles >= 32 * static_cast<int64_t>(num_cus()) && !path_flag(kernel_path().no_rows64_queue)) {
-        hipLaunchKernelGGL((k_rows64<FP8, ACT, 1, RES, XQ, FIXED, 16>), dim3(static_cast<unsigned>(num_cus())),
-                           dim3(1024), 0, st, a);
-        return;
+    if constexpr (!(RES && XQ == 2)) {
+        if (ntiles >= 32 * static_cast<int64_t>(num_cus()) && !path_flag(kernel_path().no_rows64_queue)) {
+            hipLaunchKernelGGL((k_rows64<FP8, ACT, 1, RES, XQ, FIXED, 16>), dim3(static_cast<unsigned>(num_cus())),
+                               dim3(1024), 0, st, a);
+            return;
+        }
     }
     auto kern = k_rows64<FP8, ACT, NFQ_ROWS64_PF, RES, XQ, FIXED>;
     static const int per_cu = resident_blocks(kern);

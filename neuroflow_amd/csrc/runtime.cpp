@@ -841,12 +841,16 @@ int order_run(nflow_runtime* rt, hipStream_t st) {
     return NFLOW_OK;
 }
 
+// A failed run is marked too: kernels it queued before failing use the
+// handle's workspace, and a later run on another stream must wait for them.
 int mark_run(nflow_runtime* rt, hipStream_t st, int rc) {
-    if (rc) return rc;
-    if (hipEventRecord(rt->done, st) != hipSuccess) return set_error(NFLOW_INTERNAL, "runtime_run: event record failed");
+    if (hipEventRecord(rt->done, st) != hipSuccess) {
+        if (rc) return rc;   // the run's own error first
+        return set_error(NFLOW_INTERNAL, "runtime_run: event record failed");
+    }
     rt->last_stream = st;
     rt->ran = true;
-    return NFLOW_OK;
+    return rc;
 }
 
 int create_from(nflow_ir* ir, nflow_runtime** out) {
@@ -970,6 +974,8 @@ int nflow_runtime_enable_int8_gemm_fno2d(nflow_runtime* rt) {
 int nflow_runtime_is_int8_gemm_enabled(const nflow_runtime* rt, int* enabled) {
     clear_error();
     if (!rt || !enabled) return set_error(NFLOW_INVALID_ARG, "runtime_is_int8_gemm_enabled: null argument");
+    // Under the handle's lock: EnableInt8Gemm sets the flag while it builds.
+    std::lock_guard<std::mutex> lock(const_cast<nflow_runtime*>(rt)->mu);
     *enabled = rt->int8_enabled ? 1 : 0;
     return NFLOW_OK;
 }
@@ -979,6 +985,7 @@ int nflow_runtime_layer_dispatch(const nflow_runtime* rt, int layer_index, int* 
     if (!rt || !uses_int8) return set_error(NFLOW_INVALID_ARG, "runtime_layer_dispatch: null argument");
     if (layer_index < 0 || layer_index >= rt->n_layers)
         return set_error(NFLOW_INVALID_ARG, "runtime_layer_dispatch: layer index out of range");
+    std::lock_guard<std::mutex> lock(const_cast<nflow_runtime*>(rt)->mu);
     *uses_int8 = (rt->int8_enabled && rt->lq[layer_index].int8) ? 1 : 0;
     return NFLOW_OK;
 }

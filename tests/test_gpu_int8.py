@@ -3,6 +3,7 @@ accumulators and dequantised outputs; GELU within 1e-5 rel / 1e-6 abs)."""
 import contextlib
 import ctypes
 import functools
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -170,6 +171,44 @@ def test_linear_forward_matches_reference_formulas(gpu, M, N, K, zp_a, with_sum)
     assert rc == 0
     assert _bits_equal(_host(Q.linear_forward(p, _cu(A))), ref_rows)
     assert _bits_equal(_host(Q.linear_forward(p, _cu(A[0]))), ref_rows[0])
+    rc, ref_b = O.linear_forward_batched(A, q, s, zps, b, 0.02, zp_a, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(A))), ref_b)
+
+
+@pytest.mark.parametrize("zp_a", [0, 5])
+@pytest.mark.parametrize("with_sum", [False, True])
+def test_linear_forward_scalar_formula_k4100_reference_vectors(gpu, zp_a, with_sum):
+    """Above K = 4096 the reference turns its SIMD path off (int8_gemm.cpp:218)
+    and LinearForward takes the scalar loop with its own zero-point
+    correction (:436-466); LinearForwardBatched keeps its formula
+    (:530-580).  The reference build's own outputs at K = 4100, asymmetric
+    weights, zp_A 0 / 5, with and without sum_W."""
+    fix = np.load(Path(__file__).resolve().parent / "golden" / "ref_int8_vectors.npz")
+    q, s, zps, b, X = (fix[f"lf4100_{n}"] for n in ("Wq", "sW", "zpW", "b", "X"))
+    sumW = fix["lf4100_sumW_ref"] if with_sum else None
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), scale_A=0.02, zp_A=zp_a,
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    tag = f"zp{zp_a}_sum{int(with_sum)}"
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(X))), fix[f"lf4100_rows_{tag}"])
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(X[1]))), fix[f"lf4100_rows_{tag}"][1])
+    assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(X))), fix[f"lf4100_batched_{tag}"])
+
+
+@pytest.mark.parametrize("M,N,K", [(50, 64, 4100), (37, 30, 8192), (3, 5, 4097)])
+@pytest.mark.parametrize("zp_a", [0, 5])
+@pytest.mark.parametrize("with_sum", [False, True])
+def test_linear_forward_scalar_formula_random(gpu, M, N, K, zp_a, with_sum):
+    """The K > 4096 formulas on random asymmetric layers against the oracle
+    (pinned to the reference build by the K = 4100 vectors above)."""
+    A = WL.normal(19, (M, K))
+    _, q, s, zps, sw, b = _weights(N, K, 20, zp=True)
+    sumW = (sw + (np.arange(N, dtype=np.int32) % 7) - 3).astype(np.int32) if with_sum else None
+    p = Q.Int8LinearParams(_cu(q), _cu(s), _cu(zps), _cu(b), scale_A=0.02, zp_A=zp_a,
+                           sum_W_per_row=None if sumW is None else _cu(sumW))
+    rc, ref_rows = O.linear_forward_rows(A, q, s, zps, b, 0.02, zp_a, sumW)
+    assert rc == 0
+    assert _bits_equal(_host(Q.linear_forward(p, _cu(A))), ref_rows)
     rc, ref_b = O.linear_forward_batched(A, q, s, zps, b, 0.02, zp_a, sumW)
     assert rc == 0
     assert _bits_equal(_host(Q.linear_forward_batched(p, _cu(A))), ref_b)

@@ -87,3 +87,94 @@ def test_noalloc_equals_the_allocating_entry_point(gpu, first, second):
                 np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
             else:
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_rejects_a_workspace_beyond_its_scratch(gpu):
+    """A shape whose codes and scales exceed the static scratch returns
+    NFLOW_INVALID_ARG before any launch, and leaves the output untouched."""
+    M, K, N = 80000, 1024, 64          # 80000 * 1024 + 4 * 80000 bytes > 72 MiB
+    p, _ = _layer(N, K, 990, False, None)
+    x = torch.zeros(M, K, dtype=torch.float32, device="cuda")
+    out = torch.full((M, N), 7.0, dtype=torch.float32, device="cuda")
+    ps = p.c_struct()
+    rc = _lib.lib().nflow_int8_linear_forward_per_token_noalloc(C.byref(ps), M, x.data_ptr(), out.data_ptr(),
+                                                                None, 1, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == _lib.INVALID_ARG
+    assert b"scratch" in _lib.lib().nflow_last_error()
+    assert bool((out == 7.0).all())
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """A K = 1024 call (quantise into the static scratch, then the tiled
+    GEMM) captured into a HIP graph: every replay, with eager work between
+    replays, equals the eager call bit for bit."""
+    M, K, N = 3000, 1024, 512
+    p, _ = _layer(N, K, 991, True, 2)
+    x = torch.from_numpy(WL.normal(992, (M, K))).cuda()
+    ps = p.c_struct()
+    fn = _lib.lib().nflow_int8_linear_forward_per_token_noalloc
+    want = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    _lib.check(fn(C.byref(ps), M, x.data_ptr(), want.data_ptr(), None, 2, torch.cuda.current_stream().cuda_stream),
+               "noalloc eager")
+    torch.cuda.synchronize()
+    got = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.check(fn(C.byref(ps), M, x.data_ptr(), got.data_ptr(), None, 2,
+                      torch.cuda.current_stream().cuda_stream), "noalloc captured")
+    other = torch.from_numpy(WL.normal(993, (500, K))).cuda()
+    scratch_out = torch.empty(500, N, dtype=torch.float32, device="cuda")
+    for r in range(3):
+        got.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(got), _bits(want)), f"replay {r}"
+        # Eager work on the same scratch between replays.
+        _lib.check(fn(C.byref(ps), 500, other.data_ptr(), scratch_out.data_ptr(), None, 1,
+                      torch.cuda.current_stream().cuda_stream), "noalloc between replays")
+        torch.cuda.synchronize()
+
+
+def test_noalloc_host_threads_share_one_stream(gpu):
+    """Four host threads issue no-allocation calls on one stream through the
+    C entry point (ctypes releases the GIL, so the calls overlap on the
+    host): each keeps its codes in the one static scratch, so one call's
+    quantise and product must not be split by another call's launches."""
+    import threading
+
+    K, N = 1024, 256
+    p, _ = _layer(N, K, 994, False, None)
+    ps = p.c_struct()
+    fn = _lib.lib().nflow_int8_linear_forward_per_token_noalloc
+    stream = torch.cuda.Stream()
+    xs = [torch.from_numpy(WL.normal(995 + i, (3000 + 700 * i, K))).cuda() for i in range(4)]
+    want = []
+    for x in xs:
+        w = torch.empty(x.shape[0], N, dtype=torch.float32, device="cuda")
+        _lib.check(fn(C.byref(ps), x.shape[0], x.data_ptr(), w.data_ptr(), None, 1, stream.cuda_stream), "alone")
+        torch.cuda.synchronize()
+        want.append(w)
+    outs = [[torch.empty(x.shape[0], N, dtype=torch.float32, device="cuda") for _ in range(6)] for x in xs]
+    errors = []
+
+    def worker(i):
+        try:
+            for r in range(6):
+                _lib.check(fn(C.byref(ps), xs[i].shape[0], xs[i].data_ptr(), outs[i][r].data_ptr(), None, 1,
+                              stream.cuda_stream), "noalloc thread")
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    torch.cuda.synchronize()
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors
+    for i in range(4):
+        for r in range(6):
+            assert np.array_equal(_bits(outs[i][r]), _bits(want[i])), f"thread {i} call {r}"
