@@ -362,7 +362,9 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
     chain = chained(wl)
     out_layers = wl.layers[-1:] if chain else wl.layers
     set_bytes = sum(x.nbytes for x in wl.inputs) + sum(4 * M * L.W.shape[0] for L in out_layers)
-    n_sets = args.sets or max(2, min(8, -(-1_100_000_000 // set_bytes)))
+    # At least 1.1 GB of sets, so that no step's input is still in the
+    # 256 MB last-level cache from an earlier step (C1's 16.8 MB sets: 66).
+    n_sets = args.sets or max(2, min(96, -(-1_100_000_000 // set_bytes)))
     host_in = [torch.from_numpy(x) for x in wl.inputs]
     sets = []
     for _ in range(n_sets):
@@ -507,6 +509,31 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
         else:
             roof.update({"achieved": round(g_tops, 2), "frac": round(g_tops / MFMA_PEAK_TOPS[fmt], 4)})
     roof["traffic"] = measured_traffic(kernel, name)
+    if kernel == "nfq::k_rows64" and len(layers) > 1 and not chain and graphs is None:
+        # A step's first layer reads a cold input (the sets rotate over more
+        # than the last-level cache); the later ones read their
+        # predecessor's output, partly still in that cache.  The first layer
+        # alone, timed over the same rotation (a cold input every launch),
+        # splits the step: chained average = (step - cold layer) / (layers - 1).
+        _, run0, _ = layers[0]
+        k0 = srcs[0][1]
+        reps0 = max(50, steps)
+        for i in range(3):
+            run0(sets[i % n_sets]["in"][k0].data_ptr(), sets[i % n_sets]["out"][0].data_ptr(), M, sptr)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for i in range(reps0):
+            run0(sets[i % n_sets]["in"][k0].data_ptr(), sets[i % n_sets]["out"][0].data_ptr(), M, sptr)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        cold_us = ev0.elapsed_time(ev1) * 1e3 / reps0
+        chain_us = (ms_per_step * 1e3 - cold_us) / (len(layers) - 1)
+        b0 = wl.bytes_per_layer(0)
+        roof.update({"cold_first_layer_us": round(cold_us, 3),
+                     "cold_first_layer_frac": round(b0 / (cold_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "chained_layers_avg_us": round(chain_us, 3),
+                     "chained_layers_frac": round(b0 / (chain_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "cold_first_layer_launches": reps0})
 
     copy = None
     if copy_calib:
@@ -700,8 +727,13 @@ def _config_entry(name, rec):
          "dtype": wl.layers[0].fmt, "prewarm": rec["prewarm"]}
     e.update({k: roof[k] for k in ("bound", "kernel", "kernel_avg_us", "achieved", "unit", "frac", "tops", "gbs",
                                    "bytes_per_launch", "ops_per_launch", "traffic")})
-    if "layer_avg_us" in roof:
-        e["layer_avg_us"] = roof["layer_avg_us"]
+    for k in ("layer_avg_us", "layer_level_tops", "layer_level_frac", "cold_first_layer_us", "cold_first_layer_frac",
+              "chained_layers_avg_us", "chained_layers_frac"):
+        if k in roof:
+            e[k] = roof[k]
+    e["buffer_sets"] = rec["n_sets"]
+    if rec["copy"] is not None:
+        e["copy_calibration"] = rec["copy"]
     e["parity_vs_oracle"] = rec["parity"]
     if rec["cpu"] is not None:
         e["cpu_baseline"] = rec["cpu"]
@@ -733,7 +765,10 @@ def main():
     if not args.no_cpu_baseline:
         legs = ("fp8",) if head == "c3" else ("token", "batched")
     print(f"bench.py: {head} ({args.steps} steps, {args.warmup} warm-up)", file=sys.stderr, flush=True)
-    rec = bench_workload(head, args, args.steps, args.warmup, cpu_legs=legs, copy_calib=args.copy_calib,
+    # The K = 64 layers are reported beside a same-size streaming copy over
+    # the same buffer rotation.
+    k64 = ("c1", "c2", "c3")
+    rec = bench_workload(head, args, args.steps, args.warmup, cpu_legs=legs, copy_calib=args.copy_calib or head in k64,
                          graph=args.graph)
     wl, roof = rec["wl"], rec["roofline"]
 
@@ -747,7 +782,7 @@ def main():
             print(f"bench.py: {name}", file=sys.stderr, flush=True)
             c_legs = None if args.no_cpu_baseline else (("fp8",) if name == "c3" else ("token",))
             r = bench_workload(name, args, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)),
-                               cpu_legs=c_legs)
+                               cpu_legs=c_legs, copy_calib=name in k64)
             configs[name] = _config_entry(name, r)
 
     out = {
