@@ -119,8 +119,8 @@ struct ChainSteps {
     static constexpr int pre(int k) {
         return (k == PUB0) + (k == FETCH0) + (k == PUB1) + (k == USE0) + (k == FETCH1) + (k == USE1);
     }
-    // B units: (0,0) at step 4, (0,1) at 5, (1,0) at 6, (1,1) at 7; 4 stores each.
-    static constexpr int post(int k) { return (k == 4 || k == 6 || ((k == 5 || k == 7) && TJ == 2)) ? 4 : 0; }
+    // B units: (0,0) at step 4, (0,1) at 5, (1,0) at 6, (1,1) at 7; one store each.
+    static constexpr int post(int k) { return (k == 4 || k == 6 || ((k == 5 || k == 7) && TJ == 2)) ? 1 : 0; }
 };
 
 // vmcnt at step k's wait: memory instructions issued after the stage loads
@@ -161,7 +161,6 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     __shared__ __attribute__((aligned(16))) ChainTables tb[2];
     __shared__ __attribute__((aligned(16))) float pmax[Cf::WN][BM];          // wave row maxima
     __shared__ __attribute__((aligned(16))) uint64_t pub[BM * NSLOT];       // the row tile's published words
-    __shared__ __attribute__((aligned(16))) float srow[2][BM];              // output row scales and reciprocals
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -222,27 +221,42 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     // Value v of lane l in tile (i, j): row 64 wm + 32 i + l % 32 of the block
     // tile, column 32 TJ wn + 32 j + 8 (v / 4) + 4 (l / 32) + v % 4.
     float rmax[TI];                    // running maxima of the lane's row in row block i
-    // Group g (4 values) of unit A(i, j).
-    auto a_group = [&](Acc& acc, int i, int j, int g, int par, bool live = true) {
+    float s_out[TI], inv_out[TI];      // its output row scale and the scale's reciprocal
+    // Unit A(i, j): its 16 values.
+    auto a_unit = [&](Acc& acc, int i, int j, int par, bool live = true) {
         if (!live) return;
         const ChainTables& T = tb[par];
         const float sa = T.sa[64 * wm + 32 * i + lr];
-        const int col = 32 * TJ * wn + 32 * j + 8 * g + 4 * lg;
-        const v4f sw = *reinterpret_cast<const v4f*>(T.sw + col);
-        const v4f bb = *reinterpret_cast<const v4f*>(T.bias + col);
-        float mx = (j == 0 && g == 0) ? 0.0f : rmax[i];
+        float mx = j == 0 ? 0.0f : rmax[i];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float y = activate<ACT>(dequant_bias(sw[e], sa, static_cast<float>(acc[i][j][4 * g + e]), bb[e]));
-            mx = fmaxf(mx, fabsf(y));
-            acc[i][j][4 * g + e] = __builtin_bit_cast(int32_t, y);
+        for (int g = 0; g < 4; ++g) {
+            const int col = 32 * TJ * wn + 32 * j + 8 * g + 4 * lg;
+            const v4f sw = *reinterpret_cast<const v4f*>(T.sw + col);
+            const v4f bb = *reinterpret_cast<const v4f*>(T.bias + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float y = activate<ACT>(dequant_bias(sw[e], sa, static_cast<float>(acc[i][j][4 * g + e]), bb[e]));
+                mx = fmaxf(mx, fabsf(y));
+                acc[i][j][4 * g + e] = __builtin_bit_cast(int32_t, y);
+            }
         }
         rmax[i] = mx;
     };
     // The wave's maxima of row block i (both lane halves) into LDS.
+    // v_permlane32_swap of the value with a copy of itself leaves each lane
+    // its own value and its partner's (lane l ^ 32), one in each result.
+    // The copy is opaque: given one value twice, the compiler passes one
+    // register as both operands, and the swap then returns the partner's
+    // value in both.
     auto put_wave_max = [&](int i) {
-        const float mx = fmaxf(rmax[i], __shfl_xor(rmax[i], 32));
-        pmax[wn][64 * wm + 32 * i + lr] = mx;
+        const uint32_t v = __builtin_bit_cast(uint32_t, rmax[i]);
+        uint32_t c;
+        asm volatile("v_mov_b32 %0, %1" : "=v"(c) : "v"(v));
+        const auto r = __builtin_amdgcn_permlane32_swap(v, c, false, false);
+        // Elements through scalars (bit_cast of an ext-vector element reads
+        // element 0).
+        const uint32_t r0 = r[0], r1 = r[1];
+        pmax[wn][64 * wm + 32 * i + lr] = fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
     };
     // Publish the block's maxima of row block i (the waves of column 0,
     // lanes 0..31; the others store into a zero-byte range or past it).
@@ -280,11 +294,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
             if (s2 < n_tiles_n) ok &= static_cast<uint32_t>(wds[s2] >> 32) == a.epoch;
         return ok || grow >= M;
     };
-    // Scale and reciprocal of the lane's row in row block i (into `srow`)
-    // from the published words: from `pub` (or, with from_global, global
-    // memory), re-reading global memory while any word is stale; then the
-    // row scales (column tile 0's waves of column 0, lanes 0..31) into
-    // scale_out.  Each wave reads back only the rows it wrote.
+    // Scale and reciprocal of the lane's row in row block i from the
+    // published words: from `pub` (or, with from_global, global memory),
+    // re-reading global memory while any word is stale; then the row scales
+    // (column tile 0's waves of column 0, lanes 0..31) into scale_out.
     auto row_scale = [&](const WideTile& t, int i, bool from_global) {
         const int row = 64 * wm + 32 * i + lr;
         const int64_t grow = t.m0 + row;
@@ -311,42 +324,60 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
             if (s2 < n_tiles_n) mb = static_cast<uint32_t>(wds[s2]) > mb ? static_cast<uint32_t>(wds[s2]) : mb;
         const float mx = __builtin_bit_cast(float, mb);
         const float so = (mx == 0.0f) ? 1.0f : mx / 127.0f;
-        srow[0][row] = so;
-        srow[1][row] = 1.0f / so;
+        s_out[i] = so;
+        inv_out[i] = 1.0f / so;
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const bool mine = wn == 0 && t.n0 == 0;
         const auto rs = wide_rsrc(mine ? static_cast<void*>(a.scale_out + t.m0) : nullptr, rows * 4);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, so), rs, lg ? 0x40000000 : 4 * lr,
                                               4 * (64 * wm + 32 * i), 0);
     };
-    // Group g (4 values) of unit B(i, j): codes of y / s_out, one dword.
-    auto b_group = [&](Acc& acc, int i, int j, int g, const WideTile& t) {
+    // Unit B(i, j): codes of y / s_out.  Group g of lane (lg, lr) packs the
+    // codes of columns 8 g + 4 lg .. + 3 of row lr into dword D[g]; two
+    // exchanges with the other lane half give lane lg = 0 columns 0 .. 15
+    // of the unit's 32 and lane lg = 1 columns 16 .. 31, so one 16-byte
+    // store per lane writes 32 rows x 32 bytes (as dword stores, 32 rows x
+    // 8 bytes each: 4x the L2 write requests; measured at 65536 x 1024 x
+    // 1024: 118-126 us against 123-129).
+    auto b_unit = [&](Acc& acc, int i, int j, const WideTile& t) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const auto rs = wide_rsrc(a.Cq + t.m0 * N, rows * N);
-        const int soff = (64 * wm + 32 * i) * N + t.n0 + 32 * TJ * wn + 32 * j + 8 * g;   // wave-uniform
+        const int soff = (64 * wm + 32 * i) * N + t.n0 + 32 * TJ * wn + 32 * j;   // wave-uniform
+        const int voff = lr * N + 16 * lg;
         if (!t.valid) {
-            __builtin_amdgcn_raw_buffer_store_b32(0u, rs, 0, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, rs, voff, soff, 0);
             return;
         }
-        float y[4];
+        const float inv = inv_out[i];
+        uint32_t D[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            // Through a scalar: clang's __builtin_bit_cast of an ext-vector
-            // element reads the vector's element 0.
-            const int32_t bits = acc[i][j][4 * g + e];
-            y[e] = __builtin_bit_cast(float, bits);
+        for (int g = 0; g < 4; ++g) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // Through a scalar: clang's __builtin_bit_cast of an
+                // ext-vector element reads the vector's element 0.
+                const int32_t bits = acc[i][j][4 * g + e];
+                y[e] = __builtin_bit_cast(float, bits);
+            }
+            uint64_t slow = 0;
+            int32_t q[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = quant_i8_chain(y[e], inv, slow);
+            if (slow) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) q[e] = quant_i8_token(y[e], s_out[i], inv);
+            }
+            D[g] = pack4(q[0], q[1], q[2], q[3]);
         }
-        const float inv = srow[1][64 * wm + 32 * i + lr];
-        uint64_t slow = 0;
-        int32_t q[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = quant_i8_chain(y[e], inv, slow);
-        if (slow) {
-            const float so = srow[0][64 * wm + 32 * i + lr];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) q[e] = quant_i8_token(y[e], so, inv);
-        }
-        __builtin_amdgcn_raw_buffer_store_b32(pack4(q[0], q[1], q[2], q[3]), rs, lr * N + 4 * lg, soff, kChainCodeCpol);
+        // v_permlane32_swap(D0, D2): lanes 0..31 keep D0 in the first result
+        // and get their partner's D0 in the second; lanes 32..63 get their
+        // partner's D2 in the first and keep D2 in the second -- columns
+        // 0..7 and 16..23 in order, and likewise (D1, D3) for 8..15 and 24..31.
+        const auto r02 = __builtin_amdgcn_permlane32_swap(D[0], D[2], false, false);
+        const auto r13 = __builtin_amdgcn_permlane32_swap(D[1], D[3], false, false);
+        const v4u out = {r02[0], r02[1], r13[0], r13[1]};
+        __builtin_amdgcn_raw_buffer_store_b128(out, rs, voff, soff, kChainCodeCpol);
     };
 
     // ---- the step schedule ---------------------------------------------------
@@ -394,25 +425,21 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
             // The step's drain unit, a group after each MFMA part.
             // (Nothing to drain before the first tile: its stores still go
             // out, on zero-byte ranges, for the counts.)
-            auto unit_group = [&](int g) {
-                if constexpr (k == 0) a_group(pacc, 0, 1, g, par ^ 1, pt.valid);
-                if constexpr (k == 1) a_group(pacc, 1, 0, g, par ^ 1, pt.valid);
-                if constexpr (k == 2) a_group(pacc, 1, 1, g, par ^ 1, pt.valid);
-                if constexpr (k == 4) b_group(pacc, 0, 0, g, pt);
-                if constexpr (k == 5) b_group(pacc, 0, 1, g, pt);
-                if constexpr (k == 6) b_group(pacc, 1, 0, g, pt);
-                if constexpr (k == 7) b_group(pacc, 1, 1, g, pt);
+            auto unit = [&]() {
+                if constexpr (k == 0) a_unit(pacc, 0, 1, par ^ 1, pt.valid);
+                if constexpr (k == 1) a_unit(pacc, 1, 0, par ^ 1, pt.valid);
+                if constexpr (k == 2) a_unit(pacc, 1, 1, par ^ 1, pt.valid);
+                if constexpr (k == 4) b_unit(pacc, 0, 0, pt);
+                if constexpr (k == 5) b_unit(pacc, 0, 1, pt);
+                if constexpr (k == 6) b_unit(pacc, 1, 0, pt);
+                if constexpr (k == 7) b_unit(pacc, 1, 1, pt);
             };
             const uint32_t st = st_base + Cf::STAGE * sc;
             v4i xf[4][TI], wf[4][TJ];
-            frag_read(st, 0, xf[0], wf[0]);
-            __builtin_amdgcn_sched_group_barrier(0x0100, (TI + TJ), 0);
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
-                if (hh + 1 < 4) {
-                    frag_read(st, hh + 1, xf[hh + 1], wf[hh + 1]);
-                    __builtin_amdgcn_sched_group_barrier(0x0100, TI + TJ, 0);
-                }
+                frag_read(st, hh, xf[hh], wf[hh]);
+                __builtin_amdgcn_sched_group_barrier(0x0100, TI + TJ, 0);
 #pragma unroll
                 for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -426,11 +453,9 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (TJ == 2 || (k != 0 && k != 2 && k != 5 && k != 7))
-                for (int g = 0; g < 4; ++g) unit_group(g);
+            if constexpr (TJ == 2 || (k != 0 && k != 2 && k != 5 && k != 7)) unit();
             // This tile's first unit, once its accumulators are final.
-            if constexpr (k == NK - 1)
-                for (int g = 0; g < 4; ++g) a_group(acc, 0, 0, g, par);
+            if constexpr (k == NK - 1) a_unit(acc, 0, 0, par);
             if constexpr (k == 0 || k == 2) put_wave_max(k == 0 ? 0 : 1);
             sc = sc + 1 == Cf::NS ? 0 : sc + 1;
         });
@@ -440,22 +465,18 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     auto final_drain = [&](Acc& acc, int par, const WideTile& t) {
         __builtin_amdgcn_s_waitcnt(0x070);
         asm volatile("s_barrier" ::: "memory");
-        if constexpr (TJ == 2)
-            for (int g = 0; g < 4; ++g) a_group(acc, 0, 1, g, par);
+        if constexpr (TJ == 2) a_unit(acc, 0, 1, par);
         put_wave_max(0);
-        for (int g = 0; g < 4; ++g) a_group(acc, 1, 0, g, par);
-        if constexpr (TJ == 2)
-            for (int g = 0; g < 4; ++g) a_group(acc, 1, 1, g, par);
+        a_unit(acc, 1, 0, par);
+        if constexpr (TJ == 2) a_unit(acc, 1, 1, par);
         put_wave_max(1);
         __syncthreads();
         publish(t, 0);
         publish(t, 1);
         row_scale(t, 0, true);
-        for (int j = 0; j < TJ; ++j)
-            for (int g = 0; g < 4; ++g) b_group(acc, 0, j, g, t);
+        for (int j = 0; j < TJ; ++j) b_unit(acc, 0, j, t);
         row_scale(t, 1, true);
-        for (int j = 0; j < TJ; ++j)
-            for (int g = 0; g < 4; ++g) b_group(acc, 1, j, g, t);
+        for (int j = 0; j < TJ; ++j) b_unit(acc, 1, j, t);
     };
 
 #pragma unroll
