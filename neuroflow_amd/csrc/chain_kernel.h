@@ -34,7 +34,10 @@
 //  - The drain of a tile is eight units of 16 values per lane, one per K
 //    step after the step's MFMAs (the whole drain in four of the eight
 //    steps measured 136 us against 107 us without it at 65536 x 1024 x
-//    1024; placed between the MFMA parts, the groups' registers spilled):
+//    1024).  Units split into four groups, whether placed between the
+//    MFMA parts or after them, gave wrong codes in some tiles, always in
+//    one block of lanes (l % 16 >= 12) and values (0-3, 8-11) of one unit,
+//    with nothing in the code to explain it; the drain keeps whole units.
 //    A(i, j) forms
 //    y (dequantise + bias + activation, kept in the accumulator registers as
 //    float bits) of row block i (32 rows per wave), column block j, and the
@@ -48,6 +51,10 @@
 //    (128-column tiles have no column block 1: their A(i,1) / B(i,1) are
 //    empty).  The fetch is an LDS DMA of the row block's words; the scales
 //    are read from LDS one step later.
+//  - Stage loads: A rows from the tile's row 0 with the row in the VGPR
+//    offset against the tile's valid rows (zeros past them); W rows from
+//    the matrix's start (W tiles are whole).  Stores put the lane's row in
+//    the VGPR offset, so the hardware range check drops rows past M.
 //  - Every wave issues the same memory instructions in every step (null
 //    ranges where it has nothing to move), so each wait's vmcnt is a
 //    compile-time count, as in k_gemm_wide.  The step's stage loads all go
@@ -108,6 +115,18 @@ __device__ __forceinline__ int32_t quant_i8_chain(float a, float inv, uint64_t& 
     return static_cast<int32_t>(r);
 }
 
+// The lane's index, recomputed where it is used, so that lane-dependent
+// offsets are not hoisted out of the tile loop (where each would hold a
+// register for the whole loop).  The v_mbcnt pair is ordinary compiled code,
+// so the compiler accounts for its wait states; only its zero seed is an
+// SGPR written by a one-instruction asm, which the compiler cannot see
+// through or hoist.  No VGPR is written inside asm anywhere in this kernel.
+__device__ __forceinline__ int chain_lane() {
+    uint32_t z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, z)));
+}
+
 // The drain's schedule (steps of the next tile) and the memory instructions
 // of step k issued before its stage loads (right after the barrier) and
 // after them (the codes of a B unit).
@@ -165,7 +184,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wid / Cf::WN, wn = wid % Cf::WN;
-    const int K = a.K;
+    constexpr int K = 1024;                       // chain_ok
     const int64_t M = a.M;
     const int N = a.N;
     const int n_tiles_n = N / BN;
@@ -173,19 +192,25 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     const int lr = lane & 31, lg = lane >> 5;
 
     // ---- stage loads (as k_gemm_wide) ---------------------------------------
-    // Lane offset of load c: row 8 q + lane / 8 of the step's rows (A rows,
-    // then W rows), 16-byte group (lane % 8) ^ (row % 8).
-    const int lrow = lane >> 3, lgrp = 16 * ((lane & 7) ^ (lane >> 3));
+    // Load c of a wave: rows 8 q .. 8 q + 7 of the step's rows, q = wid + W c
+    // (A rows for c < 2, as BM / 8 = 2 W, then W rows), lane row lane / 8,
+    // 16-byte group (lane % 8) ^ (row % 8).  An A load addresses from the
+    // tile's row 0, the row in the VGPR offset, against the range of the
+    // tile's valid rows (lanes past it read zeros).  W tiles are whole (N is
+    // a multiple of BN), so a W load addresses from the matrix's start: the
+    // wave's rows in the VGPR offset, the tile's and the load's in the
+    // scalar one.
+    static_assert(BM / 8 == 2 * W, "two A loads per wave");
+    const int ldma = (8 * wid + (lane >> 3)) * K + 16 * ((lane & 7) ^ (lane >> 3));
     auto dma_step = [&](uint32_t st, const WideTile& t, int step) {
         const int64_t rows_a = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
-        const int64_t rows_w = t.valid ? (N - t.n0 < BN ? N - t.n0 : BN) : 0;
         const v4u ds_a = wide_desc(a.Aq + t.m0 * K, rows_a * K);
-        const v4u ds_w = wide_desc(a.W + static_cast<int64_t>(t.n0) * K, rows_w * K);
+        const v4u ds_w = wide_desc(a.W, static_cast<int64_t>(N) * K);
 #pragma unroll
         for (int c = 0; c < NL; ++c) {
-            const int q = wid + W * c;
-            wide_dma(q < BM / 8 ? ds_a : ds_w, st + 1024 * q, ((q < BM / 8 ? 8 * q : 8 * q - BM) + lrow) * K + lgrp,
-                     ROW * step);
+            const uint32_t dst = st + 1024 * (wid + W * c);
+            if (c < 2) wide_dma(ds_a, dst, ldma + 8 * W * c * K, ROW * step);
+            else wide_dma(ds_w, dst, ldma, ROW * step + (t.n0 + 8 * W * (c - 2)) * K);
         }
     };
     // Tables of tile t into tb[par]: wave 0 scale_W, 1 bias, 2 the row
@@ -242,36 +267,36 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
         }
         rmax[i] = mx;
     };
-    // The wave's maxima of row block i (both lane halves) into LDS.
-    // v_permlane32_swap of the value with a copy of itself leaves each lane
-    // its own value and its partner's (lane l ^ 32), one in each result.
-    // The copy is opaque: given one value twice, the compiler passes one
-    // register as both operands, and the swap then returns the partner's
-    // value in both.
+    // The wave's maxima of row block i (both lane halves) into LDS.  The
+    // partner's value (lane l ^ 32) comes from two v_permlane32_swap with
+    // zero: swap(v, 0) gives lanes 0..31 the value of lanes 32..63 in its
+    // second result (zero in lanes 32..63), swap(0, v) gives lanes 32..63
+    // the value of lanes 0..31 in its first (zero in lanes 0..31).
     auto put_wave_max = [&](int i) {
         const uint32_t v = __builtin_bit_cast(uint32_t, rmax[i]);
-        uint32_t c;
-        asm volatile("v_mov_b32 %0, %1" : "=v"(c) : "v"(v));
-        const auto r = __builtin_amdgcn_permlane32_swap(v, c, false, false);
+        const auto lo_gets = __builtin_amdgcn_permlane32_swap(v, 0u, false, false);
+        const auto hi_gets = __builtin_amdgcn_permlane32_swap(0u, v, false, false);
         // Elements through scalars (bit_cast of an ext-vector element reads
         // element 0).
-        const uint32_t r0 = r[0], r1 = r[1];
-        pmax[wn][64 * wm + 32 * i + lr] = fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1));
+        const uint32_t from_hi = lo_gets[1], from_lo = hi_gets[0];
+        pmax[wn][64 * wm + 32 * i + (chain_lane() & 31)] = fmaxf(rmax[i], __builtin_bit_cast(float, from_hi | from_lo));
     };
     // Publish the block's maxima of row block i (the waves of column 0,
-    // lanes 0..31; the others store into a zero-byte range or past it).
+    // lanes 0..31; the others store into a zero-byte range or past it).  The
+    // row block's offset is in the scalar offset: `part` holds whole row
+    // tiles, so a lane past the tile's valid rows still stores inside it,
+    // and words of rows past M are never read.
     auto publish = [&](const WideTile& t, int i) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
-        const int row = 64 * wm + 32 * i + lr;
-        float mx = pmax[0][row];
+        const int r0 = 64 * wm + 32 * i;
+        float mx = pmax[0][r0 + lr];
 #pragma unroll
-        for (int w2 = 1; w2 < Cf::WN; ++w2) mx = fmaxf(mx, pmax[w2][row]);
+        for (int w2 = 1; w2 < Cf::WN; ++w2) mx = fmaxf(mx, pmax[w2][r0 + lr]);
         const v2u_c word = {__builtin_bit_cast(uint32_t, mx), a.epoch};
         const auto rs = wide_rsrc(wn == 0 ? static_cast<void*>(a.part + t.m0 * NSLOT) : nullptr, rows * NSLOT * 8);
-        // Lane part in the VGPR offset (past the range for lanes 32..63),
-        // the wave-uniform part in the scalar offset.
-        __builtin_amdgcn_raw_buffer_store_b64(word, rs, lg ? 0x40000000 : lr * NSLOT * 8,
-                                              ((64 * wm + 32 * i) * NSLOT + t.n0 / BN) * 8, kChainXcdCpol);
+        const int ln = chain_lane();
+        __builtin_amdgcn_raw_buffer_store_b64(word, rs, ln >= 32 ? 0x40000000 : ln * NSLOT * 8, (r0 * NSLOT + t.n0 / BN) * 8,
+                                              kChainXcdCpol);
     };
     // DMA of row block i's published words into `pub`: per wm, 32 rows of
     // NSLOT words in PART_KB loads of 1 KB (waves 0 .. 2 PART_KB - 1; the
@@ -286,13 +311,14 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
         const uint32_t dst = mine ? wide_lds_addr(pub) + row0 * NSLOT * 8 + 1024 * half : wide_lds_addr(tb[par].spare);
         wide_dma(d, dst, 16 * lane, 0);
     };
-    // Whether the words of global row grow are this launch's.
-    auto row_words_fresh = [&](const uint64_t* wds, int64_t grow) {
+    // Whether a row's words are this launch's (or the row is past M: its
+    // words are never written).
+    auto row_words_fresh = [&](const uint64_t* wds, bool past) {
         bool ok = true;
 #pragma unroll
         for (int s2 = 0; s2 < NSLOT; ++s2)
             if (s2 < n_tiles_n) ok &= static_cast<uint32_t>(wds[s2] >> 32) == a.epoch;
-        return ok || grow >= M;
+        return ok || past;
     };
     // Scale and reciprocal of the lane's row in row block i from the
     // published words: from `pub` (or, with from_global, global memory),
@@ -300,18 +326,28 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     // (column tile 0's waves of column 0, lanes 0..31) into scale_out.
     auto row_scale = [&](const WideTile& t, int i, bool from_global) {
         const int row = 64 * wm + 32 * i + lr;
-        const int64_t grow = t.m0 + row;
+        // Past the tile's valid rows, compared in 32 bits (no 64-bit lane row).
+        const int valid_rows = t.valid ? static_cast<int>(M - t.m0 < BM ? M - t.m0 : BM) : 0;
+        const bool past = row >= valid_rows;
         uint64_t wds[NSLOT];
 #pragma unroll
         for (int s2 = 0; s2 < NSLOT; ++s2) wds[s2] = from_global ? 0 : pub[row * NSLOT + s2];
-        bool fresh = !t.valid || (!from_global && row_words_fresh(wds, grow)) || grow >= M;
+        bool fresh = !t.valid || (!from_global && row_words_fresh(wds, past)) || past;
         if (__builtin_amdgcn_ballot_w64(!fresh)) {
             const uint64_t t0 = wall_clock64();
+            // Buffer loads with the cache policy of an agent-scope atomic
+            // load (sc1), a wave-uniform descriptor and the lane's row in a
+            // 32-bit offset (no 64-bit lane address held across the tile
+            // loop); the empty asm with a memory clobber keeps them in the
+            // loop.
+            const auto rs = wide_rsrc(a.part + (t.m0 + 64 * wm + 32 * i) * NSLOT, 32 * NSLOT * 8);
             while (!fresh) {
+                asm volatile("" ::: "memory");
 #pragma unroll
                 for (int s2 = 0; s2 < NSLOT; ++s2)
-                    wds[s2] = __hip_atomic_load(a.part + grow * NSLOT + s2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                fresh = row_words_fresh(wds, grow);
+                    wds[s2] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                                               rs, (chain_lane() & 31) * NSLOT * 8 + 8 * s2, 0, kChainXcdCpol));
+                fresh = row_words_fresh(wds, past);
                 if (!fresh && static_cast<int64_t>(wall_clock64() - t0) > a.spin_limit) {
                     __hip_atomic_store(a.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     fresh = true;
@@ -328,9 +364,12 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
         inv_out[i] = 1.0f / so;
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const bool mine = wn == 0 && t.n0 == 0;
+        // The row in the VGPR offset (the range check sees it).
+        const int r0 = 64 * wm + 32 * i;
         const auto rs = wide_rsrc(mine ? static_cast<void*>(a.scale_out + t.m0) : nullptr, rows * 4);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, so), rs, lg ? 0x40000000 : 4 * lr,
-                                              4 * (64 * wm + 32 * i), 0);
+        const int ln = chain_lane();
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, so), rs, (ln >= 32 ? 0x40000000 : 4 * ln) + 4 * r0,
+                                              0, 0);
     };
     // Unit B(i, j): codes of y / s_out.  Group g of lane (lg, lr) packs the
     // codes of columns 8 g + 4 lg .. + 3 of row lr into dword D[g]; two
@@ -342,8 +381,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     auto b_unit = [&](Acc& acc, int i, int j, const WideTile& t) {
         const int64_t rows = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const auto rs = wide_rsrc(a.Cq + t.m0 * N, rows * N);
-        const int soff = (64 * wm + 32 * i) * N + t.n0 + 32 * TJ * wn + 32 * j;   // wave-uniform
-        const int voff = lr * N + 16 * lg;
+        // The row in the VGPR offset (the range check sees it), the column
+        // within the row in the scalar offset.
+        const int soff = t.n0 + 32 * TJ * wn + 32 * j;   // wave-uniform
+        const int ln = chain_lane();
+        const int voff = ((ln & 31) + 64 * wm + 32 * i) * N + 16 * (ln >> 5);
         if (!t.valid) {
             __builtin_amdgcn_raw_buffer_store_b128(v4u{0u, 0u, 0u, 0u}, rs, voff, soff, 0);
             return;

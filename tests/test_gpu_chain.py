@@ -107,6 +107,33 @@ def test_codes_layer_all_zero_rows_and_ties(gpu):
     _no_faults()
 
 
+@pytest.mark.parametrize("M,N", [(1, 1024), (100, 512), (129, 1024), (1000, 256), (4097, 1024), (33000, 1024)])
+def test_codes_layer_writes_only_its_rows(gpu, M, N):
+    """Outputs as views at the start of larger buffers (256 more rows, so a
+    stray write of a partial row tile stays inside them): every element past
+    row M keeps its sentinel, and the rows equal a plain call's."""
+    K = 1024
+    x = WL.normal(7200 + M, (M, K))
+    q_in, s_in, _ = O.quantise_per_token_i8(x)
+    p, _ = _layer(N, K, 7210 + N)
+    big_q = torch.full((M + 256, N), 90, dtype=torch.int8, device="cuda")
+    big_s = torch.full((M + 256,), -7.0, dtype=torch.float32, device="cuda")
+    cq, cs = Q.linear_forward_codes(p, _cu(q_in), _cu(s_in), "relu", out=(big_q[:M], big_s[:M]))
+    assert bool((big_q[M:] == 90).all()), "codes written past row M"
+    assert bool((big_s[M:] == -7.0).all()), "row scales written past row M"
+    cq2, cs2 = Q.linear_forward_codes(p, _cu(q_in), _cu(s_in), "relu")
+    assert np.array_equal(_host(cq), _host(cq2))
+    assert np.array_equal(_bits(_host(cs)), _bits(_host(cs2)))
+    # A fused chain's fp32 output likewise.
+    ps = [_layer(1024, K, 7230)[0], _layer(256, 1024, 7240)[0]]
+    xin = _cu(x)
+    big_y = torch.full((M + 256, 256), -3.0, dtype=torch.float32, device="cuda")
+    y = Q.mlp_forward_per_token(ps, xin, ["relu", "none"], out=big_y[:M])
+    assert bool((big_y[M:] == -3.0).all()), "chain output written past row M"
+    assert np.array_equal(_bits(_host(y)), _bits(_host(_layer_by_layer(ps, ["relu", "none"], xin))))
+    _no_faults()
+
+
 def _chain_params(wl):
     ps, ref = [], []
     for l, L in enumerate(wl.layers):
