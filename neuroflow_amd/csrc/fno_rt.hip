@@ -299,6 +299,35 @@ __device__ __forceinline__ float apply_fq_lds(float v, const FakeQuant& q, const
     return v;
 }
 
+// x2_fake_quant with the per-tensor scale's reciprocal inv = fl(1 / s)
+// computed once (inv_ok: inv a normal float).  t = v * inv is within
+// 1.5 * 2^-23 |t| of the quotient fl(v / s), so while |t| is farther than
+// 2^-20 |t| from the nearest half-integer, rint(t) equals round(fl(v / s))
+// (the two rounding rules differ only on ties) and the rest of the
+// fake-quant follows unchanged; otherwise (near a tie, |t| >= 2^22, NaN,
+// Inf) the exact division.
+__device__ __forceinline__ float x2_fake_quant_inv(float v, float s, float inv, bool inv_ok, float zpf) {
+    const float t = v * inv;
+    const float at = fabsf(t);
+    const float dist = fabsf(__builtin_amdgcn_fractf(at) - 0.5f);
+    if (!(inv_ok && dist > __builtin_fmaf(at, 0x1p-20f, 0x1p-40f))) return x2_fake_quant(v, s, zpf);
+    float q = rintf(t) + zpf;
+    q = q < -128.0f ? -128.0f : q;
+    q = q > 127.0f ? 127.0f : q;
+    return (q - zpf) * s;
+}
+
+// The reciprocal of a per-tensor scale and whether it is a normal float.
+struct ScaleInv {
+    float inv;
+    bool ok;
+};
+__device__ __forceinline__ ScaleInv scale_inv(float s) {
+    const float inv = 1.0f / s;
+    const float a = fabsf(inv);
+    return {inv, a >= 0x1p-126f && a <= 0x1.fffffep+127f};
+}
+
 // Copies a step table into LDS; every thread of the block must call it.
 __device__ __forceinline__ void stage_steps(float* steps, const float* thr) {
     if (threadIdx.x < 15) steps[threadIdx.x] = thr[threadIdx.x];
@@ -640,40 +669,79 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
 // The snaps read their step tables from LDS, one entry per element
 // (snap_exponent_binade); the runtime checks the one-step-per-binade layout
 // of the table at creation.
+// Each thread's elements of a tile are loaded together (every load of a
+// phase issued before the first is waited for), then transposed or
+// computed; the stores follow all of the phase's results.  Loaded one at a
+// time, each element's load latency stood in front of its exact GELU (94.6
+// us a layer at 256 x 1024 x 64 on 64-token tiles, 77.7 us now).
 template <int TT>
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
+    constexpr int PER = TT * 64 / 256;  // elements per thread and tile
+    static_assert(PER * 256 == TT * 64, "tile size");
     __shared__ float tx1[64][TT + 1];  // x1, then (in place, same thread) the new h
     __shared__ float thr_x2[16], thr_next[16];
     const int n = a.n, w = a.w;
     if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
     stage_steps(thr_next, a.fq_next.thr);
+    const ScaleInv inv_x2 = scale_inv(a.scale), inv_next = scale_inv(a.fq_next.scale);
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, w, tl); id += gridDim.x) {
-        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+        // x1 (channel-major) into LDS.
+        float v[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
             const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
-            if (t < n && c < w) tx1[cr][tr] = a.x1c[(tl.s * w + c) * n + t];
+            v[q] = (t < n && c < w) ? a.x1c[(tl.s * w + c) * n + t] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
+            tx1[i / TT][i % TT] = v[q];
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+        // x2 (token-major), then the tail of each element.
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
+            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            v[q] = (t < n && c < w) ? a.x2[(tl.s * n + t) * w + c] : 0.0f;
+        }
+        // All results before any store: a store is counted with the loads,
+        // and the waits the compiler places where the per-launch branches
+        // below join are full ones, which would hold each element behind
+        // the previous element's store.
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
+            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
+            float x2 = v[q];
+            if (a.kind == 1) {
+                x2 = x2_fake_quant_inv(x2, a.scale, inv_x2.inv, inv_x2.ok, a.zpf);
+            } else if (a.kind == 2) {
+                const bool ok = t < n && c < w;
+                const int64_t p = static_cast<int64_t>(ok ? c : 0) * n + (ok ? t : 0);
+                x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
+            } else if (a.kind == 3) {
+                x2 = log2_snap(x2, a.scale, thr_x2);
+            }
+            const float y = rt_activate(tx1[cr][tr] + x2, a.act);
+            v[q] = a.fq_next.on == 1 ? x2_fake_quant_inv(y, a.fq_next.scale, inv_next.inv, inv_next.ok, a.fq_next.zpf)
+                                     : apply_fq_lds(y, a.fq_next, thr_next);
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
             const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) {
-                const int64_t o = (tl.s * n + t) * w + c;
-                float x2 = a.x2[o];
-                if (a.kind == 1) {
-                    x2 = x2_fake_quant(x2, a.scale, a.zpf);
-                } else if (a.kind == 2) {
-                    const int64_t p = static_cast<int64_t>(c) * n + t;
-                    x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
-                } else if (a.kind == 3) {
-                    x2 = log2_snap(x2, a.scale, thr_x2);
-                }
-                const float hv = apply_fq_lds(rt_activate(tx1[cr][tr] + x2, a.act), a.fq_next, thr_next);
-                a.h[o] = hv;
-                tx1[cr][tr] = hv;
+                a.h[(tl.s * n + t) * w + c] = v[q];
+                tx1[cr][tr] = v[q];
             }
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < TT * 64; i += 256) {
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int i = threadIdx.x + 256 * q;
             const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
             if (t < n && c < w) a.hc[(tl.s * w + c) * n + t] = tx1[cr][tr];
         }
@@ -857,13 +925,17 @@ hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t
     return hipGetLastError();
 }
 
+// The tail on 32-token tiles (eight elements per thread: 103 VGPRs, four
+// waves per SIMD; 64-token tiles held 153 VGPRs, three waves per SIMD, and
+// ran 96.8 us against 77.7 us at 256 x 1024 x 64, 359 us against 302 us
+// for the FNO2d model's tail), or 8-token tiles for a small batch.
 hipError_t launch_post(const PostArgs& a, hipStream_t st) {
     if (a.samples <= 0) return hipSuccess;
-    if (small_tiles(a.samples, a.n, a.w))
+    if (tile_count(a.samples, a.n, a.w, 32) < 2 * static_cast<int64_t>(num_cus()))
         hipLaunchKernelGGL(k_post_rt<8>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 8), 1, 8)), dim3(256), 0, st,
                            a);
     else
-        hipLaunchKernelGGL(k_post_rt<64>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 64), 1, 8)), dim3(256), 0,
+        hipLaunchKernelGGL(k_post_rt<32>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 32), 1, 8)), dim3(256), 0,
                            st, a);
     return hipGetLastError();
 }

@@ -52,6 +52,12 @@ CASES = [
     (2, 2048, 1, 1, 20, 16, 2, 1, False, ["fp8", "tensor"], True),
     (1, 8192, 2, 3, 8, 32, 1, 1, False, ["tensor"], True),
     (8, 1024, 1, 1, 64, 16, 4, 1, False, ["tensor"], True),
+    # Batches large enough for the layer tail's 32-token tiles (at least
+    # two tiles per CU): whole tiles, a partial channel tile (width 40) with
+    # every x2 kind, and half-filled token tiles (16 points).
+    (20, 1024, 1, 1, 64, 16, 2, 1, False, ["tensor"], True),
+    (40, 1024, 1, 1, 40, 16, 3, 1, True, ["token", "tensor", "fp8"], True),
+    (600, 16, 2, 1, 8, 4, 2, 1, False, ["fp8", "tensor"], True),
 ]
 
 
