@@ -512,28 +512,35 @@ def bench_workload(name, args, steps, warmup, cpu_legs=None, copy_calib=False, g
     if kernel == "nfq::k_rows64" and len(layers) > 1 and not chain and graphs is None:
         # A step's first layer reads a cold input (the sets rotate over more
         # than the last-level cache); the later ones read their
-        # predecessor's output, partly still in that cache.  The first layer
-        # alone, timed over the same rotation (a cold input every launch),
-        # splits the step: chained average = (step - cold layer) / (layers - 1).
-        _, run0, _ = layers[0]
-        k0 = srcs[0][1]
-        reps0 = max(50, steps)
-        for i in range(3):
-            run0(sets[i % n_sets]["in"][k0].data_ptr(), sets[i % n_sets]["out"][0].data_ptr(), M, sptr)
+        # predecessor's output, partly still in that cache.  The same steps
+        # again, over the same rotation, with an event after every layer
+        # split each step into its layers.  Each event leaves a gap before
+        # the next launch (C2: the four layers so timed sum to ~14 us more
+        # than the step), so the excess over the step's own time
+        # (ms_per_step) is taken off every layer in equal parts; the kernel
+        # trace's per-launch durations are the direct measurement.
+        nl = len(layers)
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(nl + 1)] for _ in range(steps)]
         torch.cuda.synchronize()
-        ev0.record(stream)
-        for i in range(reps0):
-            run0(sets[i % n_sets]["in"][k0].data_ptr(), sets[i % n_sets]["out"][0].data_ptr(), M, sptr)
-        ev1.record(stream)
+        for i in range(steps):
+            b = sets[i % n_sets]
+            evs[i][0].record(stream)
+            for l, (_, run, _) in enumerate(layers):
+                kind, k = srcs[l]
+                src = b["in"][k] if kind == "input" else b["out"][k]
+                run(src.data_ptr(), b["out"][l].data_ptr(), M, sptr)
+                evs[i][l + 1].record(stream)
         torch.cuda.synchronize()
-        cold_us = ev0.elapsed_time(ev1) * 1e3 / reps0
-        chain_us = (ms_per_step * 1e3 - cold_us) / (len(layers) - 1)
+        per = [[evs[i][l].elapsed_time(evs[i][l + 1]) * 1e3 for i in range(steps)] for l in range(nl)]
+        gap_us = max(0.0, (sum(sum(x) for x in per) / steps - ms_per_step * 1e3) / nl)
+        cold_us = sum(per[0]) / steps - gap_us
+        chain_us = sum(sum(x) for x in per[1:]) / (steps * (nl - 1)) - gap_us
         b0 = wl.bytes_per_layer(0)
         roof.update({"cold_first_layer_us": round(cold_us, 3),
                      "cold_first_layer_frac": round(b0 / (cold_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "chained_layers_avg_us": round(chain_us, 3),
                      "chained_layers_frac": round(b0 / (chain_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "cold_first_layer_launches": reps0})
+                     "layer_split_steps": steps, "layer_split_event_gap_us": round(gap_us, 3)})
 
     copy = None
     if copy_calib:
@@ -728,7 +735,7 @@ def _config_entry(name, rec):
     e.update({k: roof[k] for k in ("bound", "kernel", "kernel_avg_us", "achieved", "unit", "frac", "tops", "gbs",
                                    "bytes_per_launch", "ops_per_launch", "traffic")})
     for k in ("layer_avg_us", "layer_level_tops", "layer_level_frac", "cold_first_layer_us", "cold_first_layer_frac",
-              "chained_layers_avg_us", "chained_layers_frac"):
+              "chained_layers_avg_us", "chained_layers_frac", "layer_split_event_gap_us"):
         if k in roof:
             e[k] = roof[k]
     e["buffer_sets"] = rec["n_sets"]

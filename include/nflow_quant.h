@@ -219,8 +219,11 @@ int nflow_int8_linear_forward_quantised(const nflow_int8_linear_params* p, int64
  * 127 (1.0f for an all-zero row), C_q[m][n] = round-half-away(y[m][n] /
  * scale_C[m]) -- bit for bit, without y ever reaching memory when the layer
  * is symmetric (zp_W and sum_W_per_row NULL), in_features = 1024 and
- * out_features a multiple of 256 up to 1024; other layers compute y into a
- * stream-ordered buffer first.  No single reference function: it is one
+ * out_features a multiple of 256 up to 1024, and the stream is not the
+ * per-thread default stream; other calls compute y into a stream-ordered
+ * buffer first (the same bits).  On a stream being captured into a graph it
+ * returns NFLOW_UNSUPPORTED_OP and does nothing (the no-allocation entry
+ * point below is the capturable form).  No single reference function: it is one
  * step of a chain of per-token layers (the DeepONet branch and trunk MLPs,
  * cpp/src/fno.cpp:1318-1341, 1364-1386, on the INT8 path of
  * int8_gemm.cpp:201-470), where the next layer's per-token quantise
@@ -235,10 +238,14 @@ int nflow_int8_linear_forward_codes(const nflow_int8_linear_params* p, int64_t M
  * layers[l], h, activations[l]) for l = 0 .. n_layers - 1; y = h.  Bit for
  * bit that sequence.  When every layer is symmetric (zp_W and sum_W_per_row
  * NULL), layers[0].in_features = 1024 and every hidden width is 1024 (the
- * last layer's out_features any), the hidden activations stay int8 codes +
- * row scales (nflow_int8_linear_forward_codes) and only y is fp32; else the
- * layers run one by one through fp32 buffers.  layers[l + 1].in_features !=
- * layers[l].out_features -> NFLOW_SHAPE_MISMATCH. */
+ * last layer's out_features any), x is 16-byte aligned, M gives at least
+ * two 128 x 256 tiles per CU, and the stream is not the per-thread default
+ * stream, the hidden activations stay int8 codes + row scales
+ * (nflow_int8_linear_forward_codes) and only y is fp32; else the layers run
+ * one by one through fp32 buffers (the same bits).  On a stream being
+ * captured into a graph: NFLOW_UNSUPPORTED_OP, nothing done.
+ * layers[l + 1].in_features != layers[l].out_features ->
+ * NFLOW_SHAPE_MISMATCH. */
 int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, const int* activations,
                                      int n_layers, int64_t M, const float* x, float* y, void* stream);
 

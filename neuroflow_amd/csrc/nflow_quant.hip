@@ -1177,6 +1177,24 @@ static int chain_words(ChainState* cs, int64_t M, hipStream_t st) {
     return NFLOW_OK;
 }
 
+// The chain entry points under graph capture: refused before any
+// allocation or launch.  The fused kernel's row-maxima words would be
+// allocated and cleared inside the graph and a replay would reuse its
+// launch's epoch (an earlier replay's words reading as fresh); the
+// layer-by-layer route allocates its buffers inside the graph, and a graph
+// captured that way (both entry points, 20000 rows) took an illegal memory
+// access on its first replay, for a reason not found in this library.
+static bool stream_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+}
+
+// Whether calls on stream st may use the fused 8-bit-output kernel: not on
+// the per-thread default stream, whose one handle names a different stream
+// in each host thread, so concurrent launches would share the row-maxima
+// words.  Those calls take the layer-by-layer path (the same bits).
+static bool chain_stream_ok(hipStream_t st) { return st != hipStreamPerThread; }
+
 // Whether a layer takes the fused 8-bit-output kernel: symmetric weights
 // (no zero points, no caller sum_W: the integer terms of the formula are 0),
 // K = 1024, N a multiple of 256 up to 1024, 16-byte aligned codes.
@@ -1251,9 +1269,12 @@ int nflow_int8_linear_forward_codes(const nflow_int8_linear_params* p, int64_t M
     if (!A_q || !scale_A || !C_q || !scale_C) return set_error(NFLOW_INVALID_ARG, "linear_forward_codes: null input/output");
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
+    if (stream_capturing(st))
+        return set_error(NFLOW_UNSUPPORTED_OP, "linear_forward_codes: not available under graph capture (use "
+                                               "nflow_int8_linear_forward_per_token_noalloc)");
     const uint8_t* aq = reinterpret_cast<const uint8_t*>(A_q);
     uint8_t* cq = reinterpret_cast<uint8_t*>(C_q);
-    if (chain_layer_ok(p) && aligned(aq, 16) && aligned(cq, 4)) {
+    if (chain_layer_ok(p) && aligned(aq, 16) && aligned(cq, 4) && chain_stream_ok(st)) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess) return set_error(NFLOW_INTERNAL, "linear_forward_codes: hipGetDevice failed");
         ChainState* cs = chain_state(dev, st);
@@ -1290,6 +1311,9 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
     }
     if (M <= 0) return NFLOW_OK;
     hipStream_t st = as_stream(stream);
+    if (stream_capturing(st))
+        return set_error(NFLOW_UNSUPPORTED_OP, "mlp_forward_per_token: not available under graph capture (use "
+                                               "nflow_int8_linear_forward_per_token_noalloc per layer)");
     if (n_layers == 1) return int8_per_token(&layers[0], M, x, nullptr, y, nullptr, activations[0], nullptr, stream);
     // Fused: every layer symmetric, every layer but the last on the
     // 8-bit-output kernel (K = 1024, so every hidden width is 1024), and
@@ -1298,7 +1322,7 @@ int nflow_int8_mlp_forward_per_token(const nflow_int8_linear_params* layers, con
     // (measured at 4096 rows, K = N = 1024: 17.9 us against 11.2 us for the
     // fp32-output product, more than the quantise launch it saves).
     bool fused = aligned(x, 16) && !layers[n_layers - 1].zp_W && !layers[n_layers - 1].sum_W_per_row &&
-                 ((M + 127) / 128) * 4 >= 2 * static_cast<int64_t>(num_cus());
+                 ((M + 127) / 128) * 4 >= 2 * static_cast<int64_t>(num_cus()) && chain_stream_ok(st);
     for (int l = 0; l < n_layers - 1; ++l) fused = fused && chain_layer_ok(&layers[l]);
     if (fused) {
         const size_t codes = static_cast<size_t>(M) * 1024;

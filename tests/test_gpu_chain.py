@@ -247,3 +247,78 @@ def test_mlp_chain_rejects_bad_chains(gpu):
     x = _cu(WL.normal(8020, (10, 1024)))
     with pytest.raises(Exception, match="ShapeMismatch|in_features"):
         Q.mlp_forward_per_token([p1, p2], x, ["relu", "none"])
+
+
+@pytest.mark.skip(reason="faulted the GPU (illegal memory access) on its first replay when the chain entry points "
+                         "took a layer-by-layer route inside the capture, allocating their buffers in the graph; the "
+                         "cause was not found in the library, which now refuses capture in these entry points "
+                         "(test_chain_entry_points_refuse_graph_capture)")
+def test_chain_entry_points_under_graph_capture(gpu):
+    """Captured into a HIP graph, both chain entry points take the
+    layer-by-layer route (no row-maxima words or launch epochs recorded in
+    the graph): every replay, with new input values and eager fused calls on
+    the stream between replays, equals the eager call bit for bit."""
+    M = 20000
+    ps, acts = [], ["relu", "relu", "relu", "none"]
+    for l in range(4):
+        p, _ = _layer(1024 if l < 3 else 256, 1024, 8100 + 10 * l)
+        ps.append(p)
+    x = torch.empty(M, 1024, dtype=torch.float32, device="cuda")
+    y = torch.empty(M, 256, dtype=torch.float32, device="cuda")
+    q_in = torch.empty(M, 1024, dtype=torch.int8, device="cuda")
+    s_in = torch.empty(M, dtype=torch.float32, device="cuda")
+    cq = torch.empty(M, 1024, dtype=torch.int8, device="cuda")
+    cs = torch.empty(M, dtype=torch.float32, device="cuda")
+    x.copy_(_cu(WL.normal(8150, (M, 1024))))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        Q.mlp_forward_per_token(ps, x, acts, out=y)
+        Q.linear_forward_codes(ps[0], q_in, s_in, "relu", out=(cq, cs))
+    for r in range(3):
+        xr = _cu(WL.normal(8160 + r, (M, 1024)) * (1.0 + r))
+        qr, sr, _ = Q.quantise_per_token(xr)
+        x.copy_(xr)
+        q_in.copy_(qr)
+        s_in.copy_(sr)
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want_y = Q.mlp_forward_per_token(ps, xr, acts)              # eager, fused
+        want_q, want_s = Q.linear_forward_codes(ps[0], qr, sr, "relu")
+        assert np.array_equal(_bits(_host(y)), _bits(_host(want_y))), f"replay {r}"
+        assert np.array_equal(_host(cq), _host(want_q)), f"replay {r}"
+        assert np.array_equal(_bits(_host(cs)), _bits(_host(want_s))), f"replay {r}"
+    _no_faults()
+
+
+def test_chain_entry_points_refuse_graph_capture(gpu):
+    """On a stream being captured into a graph both chain entry points
+    return NFLOW_UNSUPPORTED_OP before allocating or launching anything (the
+    capture ends empty), and the stream works as before afterwards."""
+    import ctypes as C
+    from neuroflow_amd import _lib
+    M = 256
+    p, _ = _layer(1024, 1024, 8200)
+    ps = (_lib.Int8LinearParamsC * 2)(p.c_struct(), p.c_struct())
+    acts = (C.c_int * 2)(1, 1)
+    x = _cu(WL.normal(8210, (M, 1024)))
+    y = torch.empty(M, 1024, dtype=torch.float32, device="cuda")
+    qa, sa, _ = Q.quantise_per_token(x)
+    cq = torch.empty(M, 1024, dtype=torch.int8, device="cuda")
+    cs = torch.empty(M, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    L = _lib.lib()
+    rcs = []
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sp = torch.cuda.current_stream().cuda_stream
+        rcs.append(L.nflow_int8_mlp_forward_per_token(ps, acts, 2, M, x.data_ptr(), y.data_ptr(), sp))
+        rcs.append(L.nflow_int8_linear_forward_codes(C.byref(p.c_struct()), M, qa.data_ptr(), sa.data_ptr(),
+                                                     cq.data_ptr(), cs.data_ptr(), 1, sp))
+    assert rcs == [_lib.UNSUPPORTED_OP, _lib.UNSUPPORTED_OP]
+    # Eager afterwards: the same results as layer by layer.
+    y2 = Q.mlp_forward_per_token([p, p], x, ["relu", "relu"])
+    assert np.array_equal(_bits(_host(y2)), _bits(_host(_layer_by_layer([p, p], ["relu", "relu"], x))))
+    _no_faults()
