@@ -669,82 +669,97 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
 // The snaps read their step tables from LDS, one entry per element
 // (snap_exponent_binade); the runtime checks the one-step-per-binade layout
 // of the table at creation.
-// Each thread's elements of a tile are loaded together (every load of a
-// phase issued before the first is waited for), then transposed or
-// computed; the stores follow all of the phase's results.  Loaded one at a
-// time, each element's load latency stood in front of its exact GELU (94.6
-// us a layer at 256 x 1024 x 64 on 64-token tiles, 77.7 us now).
-template <int TT>
+//
+// The launch's forms are template parameters: KIND, the x2 fake-quant (0
+// none, 1 per tensor, 2 per position, 3 log2 snap); ACT (RT_ACT_RELU or
+// RT_ACT_GELU); FQN, the next layer's input fake-quant (0 off, 1 per tensor,
+// 3 log2 snap).  Chosen per element at run time, they put every element's
+// loads, stores and 64-bit index products behind uniform branches of their
+// own.  Thread x holds, per tile, channel-major elements (channel x / TT +
+// (256 / TT) q, token x % TT) and token-major elements (token x / 64 + 4 q,
+// channel x % 64), q = 0 .. PER - 1: their offsets are the thread's fixed
+// offset plus q times a per-launch stride.  Each thread's elements of a tile
+// are loaded together (every load of a phase issued before the first is
+// waited for); the stores follow all of the phase's results.
+template <int KIND, int ACT, int FQN>
+__device__ __forceinline__ float post_element(float x1, float x2, const PostArgs& a, const ScaleInv& inv_x2,
+                                              const ScaleInv& inv_next, const float* thr_x2,
+                                              const float* thr_next, float pscale, float pzp) {
+    if constexpr (KIND == 1) x2 = x2_fake_quant_inv(x2, a.scale, inv_x2.inv, inv_x2.ok, a.zpf);
+    else if constexpr (KIND == 2) x2 = x2_fake_quant(x2, pscale, pzp);
+    else if constexpr (KIND == 3) x2 = log2_snap(x2, a.scale, thr_x2);
+    float y = x1 + x2;
+    if constexpr (ACT == RT_ACT_RELU) y = y < 0.0f ? 0.0f : y;   // fno.cpp:37-40
+    else if constexpr (ACT == RT_ACT_GELU) y = gelu_fast<kGeluRefine>(y);
+    if constexpr (FQN == 1) y = x2_fake_quant_inv(y, a.fq_next.scale, inv_next.inv, inv_next.ok, a.fq_next.zpf);
+    else if constexpr (FQN == 3) y = log2_snap(y, a.fq_next.scale, thr_next);
+    return y;
+}
+
+template <int TT, int KIND, int ACT, int FQN>
 __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
-    constexpr int PER = TT * 64 / 256;  // elements per thread and tile
-    static_assert(PER * 256 == TT * 64, "tile size");
+    constexpr int PER = TT * 64 / 256;   // elements per thread and tile
+    constexpr int CSTEP = 256 / TT;      // channel rows per block pass (channel-major)
+    static_assert(PER * 256 == TT * 64 && CSTEP * TT == 256, "tile size");
     __shared__ float tx1[64][TT + 1];  // x1, then (in place, same thread) the new h
     __shared__ float thr_x2[16], thr_next[16];
     const int n = a.n, w = a.w;
     if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
     stage_steps(thr_next, a.fq_next.thr);
     const ScaleInv inv_x2 = scale_inv(a.scale), inv_next = scale_inv(a.fq_next.scale);
+    const int cm = threadIdx.x / TT, tm = threadIdx.x % TT;    // channel-major: channel, token
+    const int tk = threadIdx.x / 64, ck = threadIdx.x % 64;    // token-major: token, channel
+    const int64_t o1 = static_cast<int64_t>(cm) * n + tm, d1 = static_cast<int64_t>(CSTEP) * n;
+    const int64_t o2 = static_cast<int64_t>(tk) * w + ck, d2 = 4 * static_cast<int64_t>(w);
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, w, tl); id += gridDim.x) {
+        const int nt = n - tl.t0 < TT ? n - tl.t0 : TT;       // tokens and channels of the tile
+        const int nc = w - tl.c0 < 64 ? w - tl.c0 : 64;
+        const bool full = nt == TT && nc == 64;               // block-uniform
+        const int64_t cb = (tl.s * w + tl.c0) * static_cast<int64_t>(n) + tl.t0 + o1;
+        const int64_t tb = (tl.s * n + tl.t0) * static_cast<int64_t>(w) + tl.c0 + o2;
+        auto c_ok = [&](int q) { return full || (cm + CSTEP * q < nc && tm < nt); };
+        auto t_ok = [&](int q) { return full || (tk + 4 * q < nt && ck < nc); };
         // x1 (channel-major) into LDS.
         float v[PER];
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
-            v[q] = (t < n && c < w) ? a.x1c[(tl.s * w + c) * n + t] : 0.0f;
-        }
+        for (int q = 0; q < PER; ++q) v[q] = c_ok(q) ? a.x1c[cb + q * d1] : 0.0f;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            tx1[i / TT][i % TT] = v[q];
-        }
+        for (int q = 0; q < PER; ++q) tx1[cm + CSTEP * q][tm] = v[q];
         __syncthreads();
-        // x2 (token-major), then the tail of each element.
+        // x2 (token-major), then the tail of each element.  All results
+        // before any store: a store is counted with the loads, so a wait for
+        // a later load would also wait for every earlier store.
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
-            v[q] = (t < n && c < w) ? a.x2[(tl.s * n + t) * w + c] : 0.0f;
-        }
-        // All results before any store: a store is counted with the loads,
-        // and the waits the compiler places where the per-launch branches
-        // below join are full ones, which would hold each element behind
-        // the previous element's store.
+        for (int q = 0; q < PER; ++q) v[q] = t_ok(q) ? a.x2[tb + q * d2] : 0.0f;
+        float ps[PER], pz[PER];
+        if constexpr (KIND == 2) {
+            // Position (channel, token) of the reference's per-position
+            // tables: index channel * n + token (rows past the tile read
+            // position 0).
+            const int64_t pb = static_cast<int64_t>(tl.c0 + ck) * n + tl.t0 + tk;
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
-            float x2 = v[q];
-            if (a.kind == 1) {
-                x2 = x2_fake_quant_inv(x2, a.scale, inv_x2.inv, inv_x2.ok, a.zpf);
-            } else if (a.kind == 2) {
-                const bool ok = t < n && c < w;
-                const int64_t p = static_cast<int64_t>(ok ? c : 0) * n + (ok ? t : 0);
-                x2 = x2_fake_quant(x2, a.pos_scales[p], static_cast<float>(a.pos_zps[p]));
-            } else if (a.kind == 3) {
-                x2 = log2_snap(x2, a.scale, thr_x2);
+            for (int q = 0; q < PER; ++q) {
+                const int64_t p = t_ok(q) ? pb + 4 * q : 0;
+                ps[q] = a.pos_scales[p];
+                pz[q] = static_cast<float>(a.pos_zps[p]);
             }
-            const float y = rt_activate(tx1[cr][tr] + x2, a.act);
-            v[q] = a.fq_next.on == 1 ? x2_fake_quant_inv(y, a.fq_next.scale, inv_next.inv, inv_next.ok, a.fq_next.zpf)
-                                     : apply_fq_lds(y, a.fq_next, thr_next);
         }
 #pragma unroll
+        for (int q = 0; q < PER; ++q)
+            v[q] = post_element<KIND, ACT, FQN>(tx1[ck][tk + 4 * q], v[q], a, inv_x2, inv_next, thr_x2, thr_next,
+                                                KIND == 2 ? ps[q] : 0.0f, KIND == 2 ? pz[q] : 0.0f);
+#pragma unroll
         for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
-            if (t < n && c < w) {
-                a.h[(tl.s * n + t) * w + c] = v[q];
-                tx1[cr][tr] = v[q];
+            if (t_ok(q)) {
+                a.h[tb + q * d2] = v[q];
+                tx1[ck][tk + 4 * q] = v[q];
             }
         }
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int i = threadIdx.x + 256 * q;
-            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
-            if (t < n && c < w) a.hc[(tl.s * w + c) * n + t] = tx1[cr][tr];
-        }
+        for (int q = 0; q < PER; ++q)
+            if (c_ok(q)) a.hc[cb + q * d1] = tx1[cm + CSTEP * q][tm];
         __syncthreads();
     }
 }
@@ -925,18 +940,44 @@ hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t
     return hipGetLastError();
 }
 
-// The tail on 32-token tiles (eight elements per thread: 103 VGPRs, four
-// waves per SIMD; 64-token tiles held 153 VGPRs, three waves per SIMD, and
-// ran 96.8 us against 77.7 us at 256 x 1024 x 64, 359 us against 302 us
-// for the FNO2d model's tail), or 8-token tiles for a small batch.
+// The tail on 32-token tiles (eight elements per thread, four waves per
+// SIMD; 64-token tiles held 153 VGPRs, three waves per SIMD, and ran 96.8 us
+// against 77.7 us at 256 x 1024 x 64, 359 us against 302 us for the FNO2d
+// model's tail), or 8-token tiles for a small batch.
+template <int TT, int KIND, int ACT>
+static void launch_post_fqn(const PostArgs& a, unsigned grid, hipStream_t st) {
+    if (a.fq_next.on == 1)
+        hipLaunchKernelGGL((k_post_rt<TT, KIND, ACT, 1>), dim3(grid), dim3(256), 0, st, a);
+    else if (a.fq_next.on == 3)
+        hipLaunchKernelGGL((k_post_rt<TT, KIND, ACT, 3>), dim3(grid), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_post_rt<TT, KIND, ACT, 0>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <int TT, int KIND>
+static void launch_post_act(const PostArgs& a, unsigned grid, hipStream_t st) {
+    if (a.act == RT_ACT_GELU) launch_post_fqn<TT, KIND, RT_ACT_GELU>(a, grid, st);
+    else if (a.act == RT_ACT_RELU) launch_post_fqn<TT, KIND, RT_ACT_RELU>(a, grid, st);
+    else launch_post_fqn<TT, KIND, RT_ACT_NONE>(a, grid, st);
+}
+
+template <int TT>
+static void launch_post_tt(const PostArgs& a, hipStream_t st) {
+    const unsigned grid = grid_for(tile_count(a.samples, a.n, a.w, TT), 1, 8);
+    switch (a.kind) {
+        case 1: launch_post_act<TT, 1>(a, grid, st); break;
+        case 2: launch_post_act<TT, 2>(a, grid, st); break;
+        case 3: launch_post_act<TT, 3>(a, grid, st); break;
+        default: launch_post_act<TT, 0>(a, grid, st); break;
+    }
+}
+
 hipError_t launch_post(const PostArgs& a, hipStream_t st) {
     if (a.samples <= 0) return hipSuccess;
     if (tile_count(a.samples, a.n, a.w, 32) < 2 * static_cast<int64_t>(num_cus()))
-        hipLaunchKernelGGL(k_post_rt<8>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 8), 1, 8)), dim3(256), 0, st,
-                           a);
+        launch_post_tt<8>(a, st);
     else
-        hipLaunchKernelGGL(k_post_rt<32>, dim3(grid_for(tile_count(a.samples, a.n, a.w, 32), 1, 8)), dim3(256), 0,
-                           st, a);
+        launch_post_tt<32>(a, st);
     return hipGetLastError();
 }
 
