@@ -201,7 +201,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     // wave's rows in the VGPR offset, the tile's and the load's in the
     // scalar one.
     static_assert(BM / 8 == 2 * W, "two A loads per wave");
-    const int ldma = (8 * wid + (lane >> 3)) * K + 16 * ((lane & 7) ^ (lane >> 3));
+    // Lane l fills slot l % 8 of stage row 8 (wid + 8 c) + l / 8, which holds
+    // group (l % 8) ^ ((row >> 1) & 7) = (l % 8) ^ ((4 (wid & 1) + l / 16) & 7)
+    // (wide_lds_off's layout), the same for every load c of the wave.
+    const int ldma = (8 * wid + (lane >> 3)) * K + 16 * ((lane & 7) ^ ((4 * (wid & 1) + (lane >> 4)) & 7));
     auto dma_step = [&](uint32_t st, const WideTile& t, int step) {
         const int64_t rows_a = t.valid ? (M - t.m0 < BM ? M - t.m0 : BM) : 0;
         const v4u ds_a = wide_desc(a.Aq + t.m0 * K, rows_a * K);

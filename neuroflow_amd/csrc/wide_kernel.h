@@ -21,9 +21,13 @@
 //    whole 128-byte row segments.  (The 16 x 16 x 64 form measured slower:
 //    97-104 us against 91-97 us at 65536 x 1024 x 1024.)
 //  - K advances 128 per step.  A stage holds the step's BM + BN rows of 128
-//    bytes, with 16-byte group g of row r at slot g ^ (r & 7) (a 32-row
-//    fragment read of one group is then free of LDS bank conflicts within
-//    each 8-lane phase).  The loads are buffer_load ... lds (16 bytes per
+//    bytes, with 16-byte group g of row r at slot g ^ ((r >> 1) & 7).  A
+//    ds_read_b128 is served 16 lanes (256 bytes, 64 banks) at a time, and a
+//    fragment read of one group takes 16 consecutive rows per phase: two
+//    rows share their banks exactly when they share row parity and slot, so
+//    the slot follows r / 2.  (With slot g ^ (r & 7), rows r and r + 8
+//    collided: 43% of the LDS's active cycles were bank-conflict stalls at
+//    65536 x 1024 x 1024, none now.)  The loads are buffer_load ... lds (16 bytes per
 //    lane straight into LDS); 8 lanes cover one row's whole 128-byte line, so
 //    every instruction reads 8 full cache lines (with 64-byte steps each
 //    instruction read 16 half lines, and the loads alone took 50 us of a
@@ -91,7 +95,7 @@ typedef const __attribute__((address_space(3))) v4i* lds_v4i_ptr;
 
 // Byte offset of 16-byte group g of stage row `row` (128-byte rows).
 __device__ __forceinline__ int wide_lds_off(int row, int g) {
-    return row * 128 + 16 * (g ^ (row & 7));
+    return row * 128 + 16 * (g ^ ((row >> 1) & 7));
 }
 
 // Raw buffer descriptor as four dwords (base, stride 0, num_records, the
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     // ---- loads of one K step of a tile into a stage ------------------------
     // Load c of this wave fills 8-row region q = wid + W c (A rows first, then
     // W rows); lane l fills slot l of the region's 1 KB: row 8 q + l / 8,
-    // slot l % 8, which holds group (l % 8) ^ (row & 7) of that row.  The
+    // slot l % 8, which holds group (l % 8) ^ ((row >> 1) & 7) of that row.  The
     // offset within the tile's rows is fixed per load; the step enters as the
     // scalar offset 128 step.
     int dvoff[NL];
@@ -230,7 +234,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_gemm_wide(RowsArgs a, int n
     for (int c = 0; c < NL; ++c) {
         const int q = wid + W * c;
         const int row = 8 * q + (lane >> 3);
-        const int grp = (lane & 7) ^ (row & 7);
+        const int grp = (lane & 7) ^ ((row >> 1) & 7);
         dvoff[c] = (q < BM / 8 ? row : row - BM) * K + 16 * grp;
     }
     // Loads c0 .. c1 - 1 of the step (all of them by default).
