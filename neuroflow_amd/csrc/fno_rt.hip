@@ -201,6 +201,31 @@ __global__ __launch_bounds__(256) void k_linear_narrow(LinArgs a) {
     }
 }
 
+// k == 1 (the FNO lift), unpadded rows, n a power of two from 4 to 1024:
+// thread x makes outputs 4 (x mod n / 4) .. + 3 of each of its rows (the
+// grid's stride in quads is a multiple of n / 4, so its columns' weights and
+// bias stay in registers), one 16-byte store per row; each output is
+// fma(x, w, b), k_linear_flat's one fused step.
+__global__ __launch_bounds__(256) void k_linear_k1(LinArgs a) {
+    const int nq = a.n >> 2, lq = __builtin_ctz(static_cast<unsigned>(nq));
+    const int64_t quads = a.samples * a.rows_out * static_cast<int64_t>(nq);
+    const int64_t q0 = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int j0 = 4 * static_cast<int>(q0 & (nq - 1));
+    float wv[4], bv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        wv[e] = a.W[j0 + e];
+        bv[e] = a.b ? a.b[j0 + e] : 0.0f;
+    }
+    for (int64_t qd = q0; qd < quads; qd += static_cast<int64_t>(gridDim.x) * 256) {
+        const float x = a.x[qd >> lq];
+        v4f y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = rt_activate(__builtin_fmaf(x, wv[e], bv[e]), a.act);
+        *reinterpret_cast<v4f*>(a.y + (qd << 2)) = y;   // row (qd >> lq), column j0: index 4 qd
+    }
+}
+
 // Any shape: one thread per output.
 __global__ __launch_bounds__(256) void k_linear_flat(LinArgs a) {
     const int k = a.k, n = a.n, kplain = k - k % 8;
@@ -334,28 +359,53 @@ __device__ __forceinline__ void stage_steps(float* steps, const float* thr) {
     __syncthreads();
 }
 
-template <int TT>
+// The input fake-quant's form FQ (0 off, 1 per tensor, 3 log2 snap) is a
+// template parameter and each thread's offsets are its fixed offset plus q
+// times a per-launch stride, as in the layer tail below; thread x holds
+// token-major elements (token x / 64 + 4 q, channel x % 64) and
+// channel-major elements (channel x / TT + (256 / TT) q, token x % TT).
+template <int TT, int FQ>
 __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, int64_t samples, int n, int w,
                                                           FakeQuant fq) {
+    constexpr int PER = TT * 64 / 256;
+    constexpr int CSTEP = 256 / TT;
+    static_assert(PER * 256 == TT * 64 && CSTEP * TT == 256, "tile size");
     __shared__ float tile[64][TT + 1];
     __shared__ float steps[16];
     stage_steps(steps, fq.thr);
+    const ScaleInv inv = scale_inv(fq.scale);
+    const int cm = threadIdx.x / TT, tm = threadIdx.x % TT;
+    const int tk = threadIdx.x / 64, ck = threadIdx.x % 64;
+    const int64_t o1 = static_cast<int64_t>(cm) * n + tm, d1 = static_cast<int64_t>(CSTEP) * n;
+    const int64_t o2 = static_cast<int64_t>(tk) * w + ck, d2 = 4 * static_cast<int64_t>(w);
     Tile tl;
     for (int64_t id = blockIdx.x; tile_of<TT>(id, samples, n, w, tl); id += gridDim.x) {
-        for (int i = threadIdx.x; i < TT * 64; i += 256) {
-            const int tr = i / 64, cr = i % 64, t = tl.t0 + tr, c = tl.c0 + cr;
-            if (t < n && c < w) {
-                const int64_t o = (tl.s * n + t) * w + c;
-                const float v = apply_fq_lds(h[o], fq, steps);
-                if (fq.on != 0) h[o] = v;
-                tile[cr][tr] = v;
+        const int nt = n - tl.t0 < TT ? n - tl.t0 : TT;
+        const int nc = w - tl.c0 < 64 ? w - tl.c0 : 64;
+        const bool full = nt == TT && nc == 64;
+        const int64_t cb = (tl.s * w + tl.c0) * static_cast<int64_t>(n) + tl.t0 + o1;
+        const int64_t tb = (tl.s * n + tl.t0) * static_cast<int64_t>(w) + tl.c0 + o2;
+        auto c_ok = [&](int q) { return full || (cm + CSTEP * q < nc && tm < nt); };
+        auto t_ok = [&](int q) { return full || (tk + 4 * q < nt && ck < nc); };
+        float v[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = t_ok(q) ? h[tb + q * d2] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if constexpr (FQ == 1) v[q] = x2_fake_quant_inv(v[q], fq.scale, inv.inv, inv.ok, fq.zpf);
+            else if constexpr (FQ == 3) v[q] = log2_snap(v[q], fq.scale, steps);
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (t_ok(q)) {
+                if constexpr (FQ != 0) h[tb + q * d2] = v[q];
+                tile[ck][tk + 4 * q] = v[q];
             }
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < TT * 64; i += 256) {
-            const int cr = i / TT, tr = i % TT, t = tl.t0 + tr, c = tl.c0 + cr;
-            if (t < n && c < w) hc[(tl.s * w + c) * n + t] = tile[cr][tr];
-        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (c_ok(q)) hc[cb + q * d1] = tile[cm + CSTEP * q][tm];
         __syncthreads();
     }
 }
@@ -822,6 +872,9 @@ hipError_t launch_linear_ref(const LinArgs& a, hipStream_t st) {
             hipLaunchKernelGGL(k_linear_narrow<4>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
         else
             hipLaunchKernelGGL(k_linear_narrow<16>, dim3(grid_for(rows, 256, 8)), dim3(256), lds, st, a);
+    } else if (a.k == 1 && a.rows_in == a.rows_out && a.rows_valid == a.rows_out && a.n >= 4 && a.n <= 1024 &&
+               (a.n & (a.n - 1)) == 0 && aligned(a.y, 16)) {
+        hipLaunchKernelGGL(k_linear_k1, dim3(grid_for(rows * (a.n / 4), 256, 8)), dim3(256), 0, st, a);
     } else {
         hipLaunchKernelGGL(k_linear_flat, dim3(grid_for(rows * a.n, 256, 8)), dim3(256), 0, st, a);
     }
@@ -840,15 +893,25 @@ static bool small_tiles(int64_t samples, int n, int w) {
     return tile_count(samples, n, w, 64) < 2 * static_cast<int64_t>(num_cus());
 }
 
+template <int TT>
+static void launch_channel_major_tt(float* h, float* hc, int64_t samples, int n, int w, const FakeQuant& fq,
+                                    hipStream_t st) {
+    const dim3 grid(grid_for(tile_count(samples, n, w, TT), 1, 8));
+    if (fq.on == 1)
+        hipLaunchKernelGGL((k_to_channel_major<TT, 1>), grid, dim3(256), 0, st, h, hc, samples, n, w, fq);
+    else if (fq.on == 3)
+        hipLaunchKernelGGL((k_to_channel_major<TT, 3>), grid, dim3(256), 0, st, h, hc, samples, n, w, fq);
+    else
+        hipLaunchKernelGGL((k_to_channel_major<TT, 0>), grid, dim3(256), 0, st, h, hc, samples, n, w, fq);
+}
+
 hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,
                                    hipStream_t st) {
     if (samples <= 0) return hipSuccess;
     if (small_tiles(samples, n, w))
-        hipLaunchKernelGGL(k_to_channel_major<8>, dim3(grid_for(tile_count(samples, n, w, 8), 1, 8)), dim3(256), 0,
-                           st, h, hc, samples, n, w, fq);
+        launch_channel_major_tt<8>(h, hc, samples, n, w, fq, st);
     else
-        hipLaunchKernelGGL(k_to_channel_major<64>, dim3(grid_for(tile_count(samples, n, w, 64), 1, 8)), dim3(256),
-                           0, st, h, hc, samples, n, w, fq);
+        launch_channel_major_tt<64>(h, hc, samples, n, w, fq, st);
     return hipGetLastError();
 }
 
