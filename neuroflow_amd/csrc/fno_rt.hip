@@ -125,13 +125,31 @@ __global__ __launch_bounds__(256) void k_linear_narrow64(LinArgs a) {
     for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * 256; r0 < rows; r0 += static_cast<int64_t>(gridDim.x) * 256) {
         const int nr = rows - r0 < 256 ? static_cast<int>(rows - r0) : 256;
         const v4f* x4 = reinterpret_cast<const v4f*>(a.x + r0 * 64);
-        for (int i = threadIdx.x; i < nr * 16; i += 256) {
-            const v4f v = x4[i];
-            float* d = &xs[i >> 4][(i & 15) * 4];
-            d[0] = v[0];
-            d[1] = v[1];
-            d[2] = v[2];
-            d[3] = v[3];
+        if (nr == 256) {
+            // A whole block of rows: every load issued before the first is
+            // waited for (one at a time, each 16-byte load's latency stood in
+            // front of the next).
+            v4f v[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) v[q] = x4[threadIdx.x + 256 * q];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int i = threadIdx.x + 256 * q;
+                float* d = &xs[i >> 4][(i & 15) * 4];
+                d[0] = v[q][0];
+                d[1] = v[q][1];
+                d[2] = v[q][2];
+                d[3] = v[q][3];
+            }
+        } else {
+            for (int i = threadIdx.x; i < nr * 16; i += 256) {
+                const v4f v = x4[i];
+                float* d = &xs[i >> 4][(i & 15) * 4];
+                d[0] = v[0];
+                d[1] = v[1];
+                d[2] = v[2];
+                d[3] = v[3];
+            }
         }
         __syncthreads();
         const int t = threadIdx.x;
