@@ -738,10 +738,11 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
 // (snap_exponent_binade); the runtime checks the one-step-per-binade layout
 // of the table at creation.
 //
-// The launch's forms are template parameters: KIND, the x2 fake-quant (0
-// none, 1 per tensor, 2 per position, 3 log2 snap); ACT (RT_ACT_RELU or
-// RT_ACT_GELU); FQN, the next layer's input fake-quant (0 off, 1 per tensor,
-// 3 log2 snap).  Chosen per element at run time, they put every element's
+// The tail of fno.cpp:572-660 (the x2 fake-quant, h = act(x1 + x2)) and the
+// next layer's input fake-quant (fno.cpp:488-501).  The launch's forms are
+// template parameters: KIND, the x2 fake-quant (0 none, 1 per tensor, 2 per
+// position, 3 log2 snap); ACT (RT_ACT_NONE, RT_ACT_RELU or RT_ACT_GELU);
+// FQN, the next layer's input fake-quant (0 off, 1 per tensor, 3 log2 snap).  Chosen per element at run time, they put every element's
 // loads, stores and 64-bit index products behind uniform branches of their
 // own.  Thread x holds, per tile, channel-major elements (channel x / TT +
 // (256 / TT) q, token x % TT) and token-major elements (token x / 64 + 4 q,
