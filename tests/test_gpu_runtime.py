@@ -58,6 +58,9 @@ CASES = [
     (20, 1024, 1, 1, 64, 16, 2, 1, False, ["tensor"], True),
     (40, 1024, 1, 1, 40, 16, 3, 1, True, ["token", "tensor", "fp8"], True),
     (600, 16, 2, 1, 8, 4, 2, 1, False, ["fp8", "tensor"], True),
+    # A batch whose lift (one input channel, width 64) takes several passes
+    # of the grid: each thread's columns stay fixed from pass to pass.
+    (160, 1024, 1, 1, 64, 16, 1, 1, False, ["tensor"], True),
 ]
 
 
