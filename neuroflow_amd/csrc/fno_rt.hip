@@ -334,14 +334,6 @@ __device__ __forceinline__ float log2_snap(float x, float s, const float* thr) {
     return (sign * clamped) * s;
 }
 
-// The activation fake-quant q, the snap's step table read from LDS
-// (stage_steps), one entry per element (snap_exponent_binade).
-__device__ __forceinline__ float apply_fq_lds(float v, const FakeQuant& q, const float* steps) {
-    if (q.on == 1) return x2_fake_quant(v, q.scale, q.zpf);
-    if (q.on == 3) return log2_snap(v, q.scale, steps);
-    return v;
-}
-
 // x2_fake_quant with the per-tensor scale's reciprocal inv = fl(1 / s)
 // computed once (inv_ok: inv a normal float).  t = v * inv is within
 // 1.5 * 2^-23 |t| of the quotient fl(v / s), so while |t| is farther than
@@ -858,11 +850,31 @@ __global__ __launch_bounds__(256) void k_pad2d(const float* src, float* dst, int
     }
 }
 
-__global__ __launch_bounds__(256) void k_fq_act(float* y, int64_t n, FakeQuant fq, int act) {
+// The fake-quant's form FQ (0 off, 1 per tensor, 3 log2 snap) and the
+// activation are template parameters; four elements per thread and pass
+// (16-byte accesses) when y is 16-byte aligned, the rest one by one.
+template <int FQ, int ACT>
+__global__ __launch_bounds__(256) void k_fq_act(float* y, int64_t n, FakeQuant fq, int vec) {
     __shared__ float steps[16];
     stage_steps(steps, fq.thr);
-    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
-        y[i] = rt_activate(apply_fq_lds(y[i], fq, steps), act);
+    const ScaleInv inv = scale_inv(fq.scale);
+    auto f = [&](float v) {
+        if constexpr (FQ == 1) v = x2_fake_quant_inv(v, fq.scale, inv.inv, inv.ok, fq.zpf);
+        else if constexpr (FQ == 3) v = log2_snap(v, fq.scale, steps);
+        if constexpr (ACT == RT_ACT_RELU) v = v < 0.0f ? 0.0f : v;   // fno.cpp:37-40
+        else if constexpr (ACT == RT_ACT_GELU) v = gelu_fast<kGeluRefine>(v);
+        return v;
+    };
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    const int64_t n4 = vec ? n / 4 : 0;
+    v4f* y4 = reinterpret_cast<v4f*>(y);
+    for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n4; i += stride) {
+        v4f v = y4[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = f(v[e]);
+        y4[i] = v;
+    }
+    for (int64_t i = 4 * n4 + blockIdx.x * 256LL + threadIdx.x; i < n; i += stride) y[i] = f(y[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1016,9 +1028,23 @@ hipError_t launch_pad2d(const float* src, float* dst, int64_t samples, int h, in
     return hipGetLastError();
 }
 
+template <int FQ>
+static void launch_fq_act_fq(float* y, int64_t n, const FakeQuant& fq, int act, hipStream_t st) {
+    const int vec = aligned(y, 16) ? 1 : 0;
+    const dim3 grid(grid_for(vec ? (n + 3) / 4 : n, 256, 8));
+    if (act == RT_ACT_GELU)
+        hipLaunchKernelGGL((k_fq_act<FQ, RT_ACT_GELU>), grid, dim3(256), 0, st, y, n, fq, vec);
+    else if (act == RT_ACT_RELU)
+        hipLaunchKernelGGL((k_fq_act<FQ, RT_ACT_RELU>), grid, dim3(256), 0, st, y, n, fq, vec);
+    else
+        hipLaunchKernelGGL((k_fq_act<FQ, RT_ACT_NONE>), grid, dim3(256), 0, st, y, n, fq, vec);
+}
+
 hipError_t launch_fq_act(float* y, int64_t n, FakeQuant fq, int act, hipStream_t st) {
     if (n <= 0 || (fq.on == 0 && act == RT_ACT_NONE)) return hipSuccess;
-    hipLaunchKernelGGL(k_fq_act, dim3(grid_for(n, 256, 8)), dim3(256), 0, st, y, n, fq, act);
+    if (fq.on == 1) launch_fq_act_fq<1>(y, n, fq, act, st);
+    else if (fq.on == 3) launch_fq_act_fq<3>(y, n, fq, act, st);
+    else launch_fq_act_fq<0>(y, n, fq, act, st);
     return hipGetLastError();
 }
 
