@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void k_chain_wide(ChainArgs a, int
     // ---- stage loads (as k_gemm_wide) ---------------------------------------
     // Load c of a wave: rows 8 q .. 8 q + 7 of the step's rows, q = wid + W c
     // (A rows for c < 2, as BM / 8 = 2 W, then W rows), lane row lane / 8,
-    // 16-byte group (lane % 8) ^ (row % 8).  An A load addresses from the
+    // 16-byte group (lane % 8) ^ ((row / 2) % 8).  An A load addresses from the
     // tile's row 0, the row in the VGPR offset, against the range of the
     // tile's valid rows (lanes past it read zeros).  W tiles are whole (N is
     // a multiple of BN), so a W load addresses from the matrix's start: the
