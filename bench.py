@@ -753,8 +753,8 @@ CONFIGS = ["c1", "c2", "c3", "c4", "c5_trunk", "c5_branch"]
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one MI355X; --gpus {args.gpus} is not supported "
-              "(the path shards along rows with no collective; see the design notes)",
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (the layers shard "
+              "along rows with no collective: each GPU would run its own rows' share)",
               file=sys.stderr)
         sys.exit(2)
     if args.workload == "fno1d":
