@@ -6,7 +6,7 @@ nflow::InferenceRuntime::Create / EnableInt8Gemm / Run do for an FNO1d IR
 FNO1d::Forward (fno.cpp:408-700), in the reference's own (batch, width,
 points) layout with its permutes.
 
-TEST INFRASTRUCTURE ONLY: the checker for the device runtime; the product
+TEST INFRASTRUCTURE ONLY: the reference results for the device runtime; the product
 never imports it.
 """
 from __future__ import annotations

@@ -6,7 +6,7 @@ weight fake-quant (cpp/src/fno.cpp:997-1020 over DequantiseWeight,
 :217-289) and FNO2d::Forward (fno.cpp:777-995), in the reference's own
 (batch, width, H, W) layout with its permutes.
 
-TEST INFRASTRUCTURE ONLY: the checker for the device runtime; the product
+TEST INFRASTRUCTURE ONLY: the reference results for the device runtime; the product
 never imports it.
 """
 from __future__ import annotations

@@ -1,7 +1,7 @@
 /*
  * nflow_oracle.c -- CPU restatement of NeuroFlow's quantised inference GEMM
- * path.  TEST INFRASTRUCTURE ONLY (see nflow_oracle.h): the checker that the
- * HIP path is compared against, never the thing measured or shipped.
+ * path.  TEST INFRASTRUCTURE ONLY (see nflow_oracle.h): the reference results
+ * the HIP path is compared against, never the thing measured or shipped.
  *
  * Citations are file:line in the NeuroFlow source tree.  The arithmetic is
  * written so that gcc -O2 -ffp-contract=off rounds every float operation in

@@ -1,6 +1,6 @@
 /*
  * nflow_oracle.h -- CPU restatement of NeuroFlow's quantised inference GEMM
- * path, used ONLY as a checker.
+ * path, used ONLY as the reference results in tests.
  *
  * TEST INFRASTRUCTURE.  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load this library.  The product

@@ -2,7 +2,7 @@
 (oracle/_ref/libnflow_ref_*.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, and there only as the checker / the CPU baseline.
+bench.py's cpu_baseline leg, and there only as the reference results / the CPU baseline.
 The product never imports this module.
 
 All arrays are numpy, C-contiguous, host memory.
