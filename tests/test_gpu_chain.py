@@ -107,6 +107,36 @@ def test_codes_layer_all_zero_rows_and_ties(gpu):
     _no_faults()
 
 
+@pytest.mark.parametrize("M,special,act", [(300, "nan", "relu"), (300, "nan", "none"), (300, "inf", "relu"),
+                                           (300, "-inf", "none"), (20000, "nan", "relu"), (20000, "inf", "none")])
+def test_codes_layer_nan_and_inf_outputs(gpu, M, special, act):
+    # One column's bias NaN or +-Inf, so every row holds a NaN or an infinite
+    # output: the absmax skips NaN (the reference's `a > m`), an infinite
+    # absmax gives an infinite scale, and those values' codes take the exact
+    # path.  Codes and scales as the fp32 layer followed by the per-token
+    # quantise, on the device and in the oracle.
+    K, N = 1024, 1024
+    x = WL.normal(7400 + M, (M, K))
+    q_in, s_in, _ = O.quantise_per_token_i8(x)
+    W = WL.kaiming_uniform(7410, N, K)
+    s = O.per_channel_scales(W, 127.0)
+    wq, _ = O.quantise_weight_2d(W, s)
+    b = WL.uniform(7411, (N,), -1 / 32, 1 / 32)
+    b[5] = float(special)
+    p = Q.Int8LinearParams(W_int8=_cu(wq), scale_W=_cu(s), zp_W=None, bias=_cu(b), sum_W_per_row=None)
+    cq, cs = Q.linear_forward_codes(p, _cu(q_in), _cu(s_in), act)
+    y = Q.linear_forward_quantised(p, _cu(q_in), _cu(s_in), act)
+    q2, s2, _ = Q.quantise_per_token(y)
+    assert np.array_equal(_host(cq), _host(q2))
+    assert np.array_equal(_bits(_host(cs)), _bits(_host(s2)))
+    rows = np.unique(np.r_[0, M - 1, np.linspace(0, M - 1, 32).astype(int)])
+    y_ref, _ = O.layer_per_token_i8(x[rows], wq, s, bias=b, act=ACT[act])
+    q_ref, sc_ref, _ = O.quantise_per_token_i8(y_ref)
+    assert np.array_equal(_host(cq)[rows], q_ref)
+    assert np.array_equal(_bits(_host(cs)[rows]), _bits(sc_ref))
+    _no_faults()
+
+
 @pytest.mark.parametrize("M,N", [(1, 1024), (100, 512), (129, 1024), (1000, 256), (4097, 1024), (33000, 1024)])
 def test_codes_layer_writes_only_its_rows(gpu, M, N):
     """Outputs as views at the start of larger buffers (256 more rows, so a
