@@ -48,6 +48,10 @@ CASES = [
     (1, 256, 256, 1, 1, 64, 12, 12, 1, 1, False, ["fp8"]),
     (2, 8, 8, 1, 1, 8, 8, 5, 1, 1, False, None),            # all H rows and all W/2 + 1 bins
     (1, 4, 2, 1, 1, 4, 2, 2, 0, 1, False, ["tensor"]),       # no layers
+    # Output element counts that are not a multiple of 4 (the fake-quant
+    # passes' one-by-one remainder): 3 x 1 x 2 x 1 and 3 x 1 x 2 x 3.
+    (3, 1, 2, 1, 1, 4, 1, 2, 1, 1, False, ["tensor", "fp8"]),
+    (3, 1, 2, 2, 3, 4, 1, 2, 1, 1, True, ["fp8", "tensor"]),
 ]
 
 
