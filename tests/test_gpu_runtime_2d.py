@@ -100,6 +100,15 @@ def test_run_device_and_infer_arrays(gpu, tmp_path):
     rt.run_device(xt[:1].data_ptr(), [1, 32, 16, 2], y2.data_ptr(), [1, 32, 16, 2], stream.cuda_stream)
     torch.cuda.synchronize(dev)
     assert np.array_equal(_bits(y2.cpu().numpy()), _bits(want[:1]))
+    # An output 4 bytes past a 16-byte boundary (the output fake-quant's
+    # one-element-at-a-time form); the element before it stays untouched.
+    big = torch.full((1 + 3 * 32 * 16 * 2,), float("nan"), device=dev)
+    big[0] = 7.0
+    y3 = big[1:].view(3, 32, 16, 2)
+    rt.run_device(xt.data_ptr(), list(xt.shape), y3.data_ptr(), list(y3.shape), stream.cuda_stream)
+    torch.cuda.synchronize(dev)
+    assert np.array_equal(_bits(y3.cpu().numpy()), _bits(want))
+    assert big[0].item() == 7.0
     assert np.array_equal(_bits(ncpp.infer_arrays(str(path), x)), _bits(want))
     with pytest.raises(RuntimeError, match="input rank mismatch for op FNO2d"):
         ncpp.infer_arrays(str(path), x[0])
