@@ -105,8 +105,10 @@ const char* nflow_last_error(void);
  * "gemm_tile" (0 = the launcher's choice, else 88, 48, 44, 24 or 22) and
  * "gemm_mfma" (0 = the launcher's choice, else 16 or 32: the MFMA shape of
  * the LDS-DMA GEMM), "no_wide" (0 / 1: keep K = 512 / 1024 layers off the
- * persistent GEMM) and "no_rows64_queue" (0 / 1: the K = N = 64 layer with
- * its static tile deal instead of the per-CU tile queue).  The
+ * persistent GEMM), "no_rows64_queue" (0 / 1: the K = N = 64 layer with
+ * its static tile deal instead of the per-CU tile queue) and
+ * "no_layer_tail" (0 / 1: the FNO1d runtime's width-64 INT8 layer and its
+ * tail as two launches instead of one).  The
  * environment variables NFLOW_<NAME> set the initial values, read once at
  * the library's first launch.  Process-wide; *previous (if not NULL)
  * receives the value replaced.  Unknown names return NFLOW_INVALID_ARG. */

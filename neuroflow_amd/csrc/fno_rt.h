@@ -16,6 +16,8 @@
 
 #include <cstdint>
 
+struct nflow_layer;
+
 namespace nfq {
 
 enum RtAct { RT_ACT_NONE = 0, RT_ACT_RELU = 1, RT_ACT_GELU = 2 };
@@ -147,5 +149,27 @@ struct PostArgs {
     FakeQuant fq_next;
 };
 hipError_t launch_post(const PostArgs& a, hipStream_t st);
+
+// The INT8 local-linear layer (LinearForwardBatched + bias, int8_gemm.cpp:530-580,
+// as fno.cpp:529-536 runs it) and the layer tail in one pass at width 64:
+// x2 = (sW * sA) * D + b from the codes of h quantised with the per-tensor
+// scale sA / zero point zpA, then the tail of PostArgs (p.x2 unused), h
+// overwritten in place.  Taken when layer_tail_ok holds; the unfused pair
+// computes the same bits.
+struct LayerTailArgs {
+    PostArgs p;
+    const int8_t* W;         // (64, 64) codes, row per output channel
+    const float* sW;         // (64)
+    const float* bias;       // (64) or null
+    const int32_t* zpW;      // (64) or null
+    const int32_t* sumW;     // (64) or null
+    float sA;
+    int32_t zpA;
+};
+bool layer_tail_ok(const PostArgs& p, int in_features, int out_features);
+// The device arrays of an INT8 layer handle into a (layer.cpp): false for
+// another format.
+bool layer_int8_arrays(const nflow_layer* layer, LayerTailArgs* a, int* in_features, int* out_features);
+hipError_t launch_layer_tail(const LayerTailArgs& a, hipStream_t st);
 
 }  // namespace nfq

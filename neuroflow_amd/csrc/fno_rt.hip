@@ -17,6 +17,7 @@
 #include "fno_rt.h"
 #include "gelu_exact.h"
 #include "launch.h"
+#include "rows64_kernel.h"
 #include "snap.h"
 
 namespace nfq {
@@ -825,6 +826,138 @@ __global__ __launch_bounds__(256) void k_post_rt(PostArgs a) {
     }
 }
 
+// The INT8 local-linear layer and the tail in one pass (LayerTailArgs): on a
+// 32-token x 64-channel tile, the h tile is read once (16 bytes per thread,
+// token-major) and quantised with the per-tensor scale into LDS codes (the
+// reciprocal fast path with the exact quotient where it is not certain, as
+// k_rows64's fixed-scale form), each wave forms a 16-token x 32-channel
+// block of D with two v_mfma_i32_16x16x64_i8 (weights in registers), and the
+// dequantise + bias and the tail run in the MFMA result layout on x1 from
+// the channel-major LDS tile, where the results replace x1 for the two
+// stores.  x2 never reaches HBM: per layer 256 MB move instead of 402 MB at
+// 256 x 1024 x 64.
+template <int KIND, int ACT, int FQN, bool INT_EPI>
+__global__ __launch_bounds__(256) void k_layer_tail(LayerTailArgs la) {
+    constexpr int TT = 32, PER = TT * 64 / 256, CSTEP = 256 / TT, CODE_DW = 20;   // 64 code bytes + 16 of padding
+    const PostArgs& a = la.p;
+    __shared__ float tx1[64][TT + 1];   // x1, then (in place, same lane) the new h
+    __shared__ uint32_t codes[TT * CODE_DW];
+    __shared__ float thr_x2[16], thr_next[16];
+    __shared__ float csw[64], cbias[64];
+    __shared__ IntEpi cepi[INT_EPI ? 64 : 1];
+    const int n = a.n;                  // w == 64, n % 32 == 0 (layer_tail_ok)
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
+    if (threadIdx.x < 64) {
+        const int c = threadIdx.x;
+        csw[c] = la.sW[c];
+        cbias[c] = la.bias ? la.bias[c] : 0.0f;
+        if constexpr (INT_EPI) {
+            const uint32_t* wr = reinterpret_cast<const uint32_t*>(la.W + 64 * c);
+            int32_t sfull = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) sfull = sum_bytes_i8(wr[q], sfull);
+            cepi[c] = int_epi_consts(F_BATCHED, 64, la.zpA, la.zpW ? la.zpW[c] : 0, la.sumW ? la.sumW[c] : 0,
+                                     la.sumW != nullptr, sfull, sfull);
+        }
+    }
+    stage_steps(thr_next, a.fq_next.thr);
+    const ScaleInv inv_x2 = scale_inv(a.scale), inv_next = scale_inv(a.fq_next.scale);
+    const float fixed_inv = 1.0f / la.sA;
+    const bool fixed_exact = !(la.sA >= 0x1p-120f && la.sA <= 0x1p120f);
+    // MFMA roles: wave wid takes tokens 16 (wid & 1) .. + 15 and channels
+    // 32 (wid >> 1) .. + 31 (two 16-column tiles); lane (r, g) supplies
+    // weight row 32 (wid >> 1) + 16 ct + r and code row 16 (wid & 1) + r,
+    // bytes 16 g .. 16 g + 15, and receives token 16 (wid & 1) + r, channels
+    // 32 (wid >> 1) + 16 ct + 4 g .. + 3.
+    const int r = lane & 15, g = lane >> 4, tr = wid & 1, chh = wid >> 1;
+    v4i wop[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(la.W + (32 * chh + 16 * ct + r) * 64 + 16 * g);
+        wop[ct] = v4i{static_cast<int>(src[0]), static_cast<int>(src[1]), static_cast<int>(src[2]),
+                      static_cast<int>(src[3])};
+    }
+    // Load and store roles as the tail's: channel-major (channel x / 32 +
+    // 8 q, token x % 32), token-major (token x / 64 + 4 q, channel x % 64);
+    // the h tile's loads: token x / 16 + 16 q, channels 4 (x % 16) .. + 3.
+    const int cm = threadIdx.x / TT, tm = threadIdx.x % TT, tk = threadIdx.x / 64, ck = threadIdx.x % 64;
+    const int hq_t = threadIdx.x / 16, hq_c = 4 * (threadIdx.x % 16);
+    const int64_t o1 = static_cast<int64_t>(cm) * n + tm, d1 = static_cast<int64_t>(CSTEP) * n;
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, 64, tl); id += gridDim.x) {
+        const int64_t cb = tl.s * 64 * static_cast<int64_t>(n) + tl.t0 + o1;
+        const int64_t tb = (tl.s * n + tl.t0) * 64;
+        v4f hv[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) hv[q] = *reinterpret_cast<const v4f*>(a.h + tb + (hq_t + 16 * q) * 64 + hq_c);
+        float xv[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) xv[q] = a.x1c[cb + q * d1];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) tx1[cm + CSTEP * q][tm] = xv[q];
+        // Codes of the h tile (QuantiseActivation with the layer's scale).
+        uint32_t badm = 0;
+        int32_t cq[2][4];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bool bad;
+                cq[q][e] = quant_i8_fixed_near(hv[q][e], fixed_inv, la.zpA, bad);
+                badm |= (bad || fixed_exact) ? (1u << (4 * q + e)) : 0u;
+            }
+        if (__builtin_amdgcn_ballot_w64(badm != 0)) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (badm & (1u << (4 * q + e))) cq[q][e] = quant_i8_exact(hv[q][e], la.sA, la.zpA);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            codes[(hq_t + 16 * q) * CODE_DW + hq_c / 4] = pack4(cq[q][0], cq[q][1], cq[q][2], cq[q][3]);
+        __syncthreads();
+        // D, the dequantise + bias, and the tail of the lane's eight values.
+        const uint32_t* crow = codes + (16 * tr + r) * CODE_DW + 4 * g;
+        const v4i xo = v4i{static_cast<int>(crow[0]), static_cast<int>(crow[1]), static_cast<int>(crow[2]),
+                           static_cast<int>(crow[3])};
+        int32_t SA = 0;
+        if constexpr (INT_EPI) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) SA = sum_bytes_i8(static_cast<uint32_t>(xo[q]), SA);
+            SA = row_sum4(SA);
+        }
+        const int tok = 16 * tr + r;
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(wop[ct], xo, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int ch = 32 * chh + 16 * ct + 4 * g + v;
+                float t;
+                if constexpr (INT_EPI) t = int_epi_value(cepi[ch], acc[v], SA);
+                else t = static_cast<float>(acc[v]);
+                const float x2 = dequant_bias(csw[ch], la.sA, t, cbias[ch]);
+                float ps = 0.0f, pz = 0.0f;
+                if constexpr (KIND == 2) {
+                    const int64_t pidx = static_cast<int64_t>(ch) * n + tl.t0 + tok;
+                    ps = a.pos_scales[pidx];
+                    pz = static_cast<float>(a.pos_zps[pidx]);
+                }
+                tx1[ch][tok] = post_element<KIND, ACT, FQN>(tx1[ch][tok], x2, a, inv_x2, inv_next, thr_x2, thr_next,
+                                                            ps, pz);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < PER; ++q) a.h[tb + (tk + 4 * q) * 64 + ck] = tx1[ck][tk + 4 * q];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) a.hc[cb + q * d1] = tx1[cm + CSTEP * q][tm];
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------
 // FNO2d padding and the projection fake-quants.
 // ---------------------------------------------------------------------------
@@ -1086,6 +1219,48 @@ hipError_t launch_post(const PostArgs& a, hipStream_t st) {
         launch_post_tt<8>(a, st);
     else
         launch_post_tt<32>(a, st);
+    return hipGetLastError();
+}
+
+// The fused layer + tail: width 64, whole 32-token tiles (n a multiple of
+// 32), at least two tiles per CU, the runtime's activations (ReLU, GELU) and
+// next-input fake-quants (off, per tensor), and the layer of 64 x 64.
+bool layer_tail_ok(const PostArgs& p, int in_features, int out_features) {
+    return !path_flag(kernel_path().no_layer_tail) && p.w == 64 && in_features == 64 && out_features == 64 &&
+           p.n > 0 && p.n % 32 == 0 && tile_count(p.samples, p.n, p.w, 32) >= 2 * static_cast<int64_t>(num_cus()) &&
+           (p.act == RT_ACT_RELU || p.act == RT_ACT_GELU) && (p.fq_next.on == 0 || p.fq_next.on == 1) &&
+           p.kind >= 0 && p.kind <= 3 && aligned(p.h, 16);
+}
+
+template <int KIND, int ACT, int FQN>
+static void launch_layer_tail_epi(const LayerTailArgs& a, unsigned grid, hipStream_t st) {
+    if (a.zpA == 0 && !a.zpW)
+        hipLaunchKernelGGL((k_layer_tail<KIND, ACT, FQN, false>), dim3(grid), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_layer_tail<KIND, ACT, FQN, true>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <int KIND, int ACT>
+static void launch_layer_tail_fqn(const LayerTailArgs& a, unsigned grid, hipStream_t st) {
+    if (a.p.fq_next.on == 1) launch_layer_tail_epi<KIND, ACT, 1>(a, grid, st);
+    else launch_layer_tail_epi<KIND, ACT, 0>(a, grid, st);
+}
+
+template <int KIND>
+static void launch_layer_tail_act(const LayerTailArgs& a, unsigned grid, hipStream_t st) {
+    if (a.p.act == RT_ACT_GELU) launch_layer_tail_fqn<KIND, RT_ACT_GELU>(a, grid, st);
+    else launch_layer_tail_fqn<KIND, RT_ACT_RELU>(a, grid, st);
+}
+
+hipError_t launch_layer_tail(const LayerTailArgs& a, hipStream_t st) {
+    if (a.p.samples <= 0) return hipSuccess;
+    const unsigned grid = grid_for(tile_count(a.p.samples, a.p.n, a.p.w, 32), 1, 8);
+    switch (a.p.kind) {
+        case 1: launch_layer_tail_act<1>(a, grid, st); break;
+        case 2: launch_layer_tail_act<2>(a, grid, st); break;
+        case 3: launch_layer_tail_act<3>(a, grid, st); break;
+        default: launch_layer_tail_act<0>(a, grid, st); break;
+    }
     return hipGetLastError();
 }
 

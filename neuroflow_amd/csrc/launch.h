@@ -45,7 +45,7 @@ inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 // two kernels computing the same bits.  They are read from the environment
 // once, at the first launch (NFLOW_NO_GEMM, NFLOW_NO_ROWS64,
 // NFLOW_NO_TOKEN_GEMM, NFLOW_GEMM_REG, NFLOW_GEMM_TILE, NFLOW_GEMM_MFMA,
-// NFLOW_NO_WIDE, NFLOW_NO_ROWS64_QUEUE), and afterwards
+// NFLOW_NO_WIDE, NFLOW_NO_ROWS64_QUEUE, NFLOW_NO_LAYER_TAIL), and afterwards
 // change only through nflow_debug_set_kernel_path; a launch reads relaxed
 // atomics, never the environment.
 struct KernelPath {
@@ -57,6 +57,7 @@ struct KernelPath {
     std::atomic<int> gemm_mfma{0};   // 0: the launcher's choice, else 16 or 32
     std::atomic<int> no_wide{0};
     std::atomic<int> no_rows64_queue{0};
+    std::atomic<int> no_layer_tail{0};   // the FNO runtime's INT8 layer + tail as two launches
 };
 KernelPath& kernel_path();
 

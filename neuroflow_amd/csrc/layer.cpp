@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "nflow_quant.h"
+#include "fno_rt.h"
 #include "status.h"
 
 struct nflow_layer {
@@ -225,3 +226,21 @@ int nflow_layer_destroy(nflow_layer* layer) {
 }
 
 }  // extern "C"
+
+namespace nfq {
+
+bool layer_int8_arrays(const nflow_layer* layer, LayerTailArgs* a, int* in_features, int* out_features) {
+    if (!layer || layer->format != NFLOW_FORMAT_INT8) return false;
+    a->W = static_cast<const int8_t*>(layer->W);
+    a->sW = layer->scale_W;
+    a->bias = layer->bias;
+    // A symmetric blob's zero points are all 0: none passed, so that with
+    // zp_A = 0 every integer term of the batched formula is known to vanish.
+    a->zpW = layer->symmetric ? nullptr : layer->zp_W;
+    a->sumW = layer->sum_W;
+    *in_features = layer->in_features;
+    *out_features = layer->out_features;
+    return true;
+}
+
+}  // namespace nfq

@@ -627,13 +627,6 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
                     tw, tw + 2 * (n_pad > 1 ? n_pad - 1 : 1), b, static_cast<int>(n_pad), log2n, w, rt->modes,
                     1.0f / static_cast<float>(n_pad)};
         if (int rc = launch_check(launch_spectral(sp, st), "spectral convolution")) return rc;
-        if (q.int8 && rt->int8_enabled) {
-            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], M, H, X2, q.sa, q.zpa, st)) return rc;
-        } else {
-            LinArgs loc{H, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b,
-                        static_cast<int>(n_pad), static_cast<int>(n_pad), static_cast<int>(n_pad), w, w, RT_ACT_NONE};
-            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
-        }
         PostArgs pa{};
         pa.x2 = X2;
         pa.x1c = X1C;
@@ -652,6 +645,25 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
         std::memcpy(pa.thr, rt->thr, sizeof(pa.thr));
         pa.act = rt->act;
         pa.fq_next = in_fq(i + 1);
+        // The INT8 layer and the tail in one launch where it applies (the
+        // same bits as the two launches below).
+        LayerTailArgs lt{};
+        int lin = 0, lout = 0;
+        if (q.int8 && rt->int8_enabled && layer_int8_arrays(rt->int8_layers[i], &lt, &lin, &lout) &&
+            layer_tail_ok(pa, lin, lout)) {
+            lt.p = pa;
+            lt.sA = q.sa;
+            lt.zpA = q.zpa;
+            if (int rc = launch_check(launch_layer_tail(lt, st), "layer + tail")) return rc;
+            continue;
+        }
+        if (q.int8 && rt->int8_enabled) {
+            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], M, H, X2, q.sa, q.zpa, st)) return rc;
+        } else {
+            LinArgs loc{H, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b,
+                        static_cast<int>(n_pad), static_cast<int>(n_pad), static_cast<int>(n_pad), w, w, RT_ACT_NONE};
+            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        }
         if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
     }
     // Trim, proj_q + act, proj_out (fno.cpp:662-698).

@@ -89,6 +89,36 @@ def test_run_bit_exact(gpu, tmp_path, case):
         assert np.array_equal(_bits(y), _bits(ref_run(tmp_path, ir, x, case[3], case[10])))
 
 
+@pytest.mark.parametrize("kinds,relu", [(["tensor"], False), (["token", "tensor", "fp8"], True),
+                                        (["fp8", "token"], False)])
+def test_layer_tail_fused_equals_two_launches(gpu, tmp_path, kinds, relu):
+    """The width-64 INT8 layer and its tail in one launch (k_layer_tail)
+    against the two launches (k_rows64 + k_post_rt, kernel path
+    no_layer_tail) and the oracle: every x2 fake-quant kind, with and
+    without zero points on the layer input."""
+    case = (20, 1024, 1, 1, 64, 16, 3, 1, relu, kinds, True)
+    ncpp = load()
+    ir, x, m = _model(case)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    want = OF.forward(m, x)
+    L = _lib.lib()
+    outs = []
+    for flag in (0, 1):
+        prev = C.c_int(0)
+        _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", flag, C.byref(prev)), "kernel path")
+        try:
+            rt = ncpp.InferenceRuntime(str(path))
+            rt.enable_int8_gemm()
+            y = np.zeros((x.shape[0], x.shape[1], 1), np.float32)
+            rt.run(x, y)
+            outs.append(y)
+        finally:
+            _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", prev.value, None), "kernel path")
+    for y in outs:
+        assert np.array_equal(_bits(y), _bits(want)), int((_bits(y) != _bits(want)).sum())
+
+
 def test_dispatch_matches_the_reference_decision(gpu, tmp_path):
     case = (2, 64, 3, 1, 12, 8, 4, 1, False, ["tensor", "token", "fp8"], True)
     ir, x, m = _model(case)
