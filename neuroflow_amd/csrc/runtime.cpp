@@ -780,20 +780,9 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
         irows.fill = zf;
         irows.fill_period = Hp;
         if (int rc = launch_check(launch_irfft_rows(irows, st), "inverse row FFT")) return rc;
-        // Local linear (fno.cpp:906-932): fp32 as in the reference, or, after
-        // the FNO2d INT8 opt-in, FNO1d's INT8 branch (LinearForwardBatched
-        // with the input key's per-tensor qparam, then + bias).
         const int ip = static_cast<int>(pts);
-        if (q.int8 && rt->int8_enabled) {
-            if (b * pts > INT32_MAX)
-                return set_error(NFLOW_INVALID_ARG, "runtime: batch * points exceeds the batched API's int");
-            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], b * pts, Hb, X2, q.sa, q.zpa, st))
-                return rc;
-        } else {
-            LinArgs loc{Hb, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b, ip, ip, ip, w,
-                        w, RT_ACT_NONE};
-            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
-        }
+        if (q.int8 && rt->int8_enabled && b * pts > INT32_MAX)
+            return set_error(NFLOW_INVALID_ARG, "runtime: batch * points exceeds the batched API's int");
         // Tail (fno.cpp:934-945).
         PostArgs pa{};
         pa.x2 = X2;
@@ -808,6 +797,28 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
         pa.zpf = static_cast<float>(q.x2_zp);
         std::memcpy(pa.thr, rt->thr, sizeof(pa.thr));
         pa.act = rt->act;
+        // The INT8 layer and the tail in one launch where it applies (as FNO1d).
+        LayerTailArgs lt{};
+        int lin = 0, lout = 0;
+        if (q.int8 && rt->int8_enabled && layer_int8_arrays(rt->int8_layers[i], &lt, &lin, &lout) &&
+            layer_tail_ok(pa, lin, lout)) {
+            lt.p = pa;
+            lt.sA = q.sa;
+            lt.zpA = q.zpa;
+            if (int rc = launch_check(launch_layer_tail(lt, st), "layer + tail")) return rc;
+            continue;
+        }
+        // Local linear (fno.cpp:906-932): fp32 as in the reference, or, after
+        // the FNO2d INT8 opt-in, FNO1d's INT8 branch (LinearForwardBatched
+        // with the input key's per-tensor qparam, then + bias).
+        if (q.int8 && rt->int8_enabled) {
+            if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], b * pts, Hb, X2, q.sa, q.zpa, st))
+                return rc;
+        } else {
+            LinArgs loc{Hb, rt->dw("locs." + si + ".weight"), rt->dw("locs." + si + ".bias"), X2, b, ip, ip, ip, w,
+                        w, RT_ACT_NONE};
+            if (int rc = launch_check(launch_linear_ref(loc, st), "local linear")) return rc;
+        }
         if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
     }
     // Trim (fno.cpp:946-964), proj_q + fake-quant + act, proj_out + fake-quant (fno.cpp:966-993).

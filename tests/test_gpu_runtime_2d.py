@@ -152,6 +152,8 @@ INT8_CASES = [
     (2, 16, 8, 1, 2, 8, 3, 3, 4, 1, True, ["tensor", "fp8"]),      # fp8 inputs keep those layers fp32
     (1, 4, 4, 1, 1, 4, 2, 2, 2, 8, False, ["tensor"]),             # padded
     (2, 64, 64, 1, 1, 64, 12, 12, 2, 1, False, ["tensor"]),
+    # Enough 32-point tiles for the layer and its tail in one launch.
+    (4, 64, 64, 1, 1, 64, 12, 12, 2, 1, True, ["tensor"]),
 ]
 
 
