@@ -61,6 +61,11 @@ struct FakeQuant {
 // input fake-quant fq applied to both when on.
 hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,
                                    hipStream_t st);
+// The lift with one input channel (LinArgs with k = 1, unpadded rows, no
+// activation) followed by launch_to_channel_major, in one pass: h and hc
+// as the two launches write them.
+hipError_t launch_lift_layout(const float* x, const float* W, const float* b, float* h, float* hc, int64_t samples,
+                              int n, int w, FakeQuant fq, hipStream_t st);
 
 // Spectral convolution of fno.cpp:164-207 on channel-major hc: forward FFT
 // of every channel (radix-2, fft.cpp:48-84) keeping bins 0 .. modes-1 in

@@ -421,6 +421,61 @@ __global__ __launch_bounds__(256) void k_to_channel_major(float* h, float* hc, i
     }
 }
 
+// The lift with one input channel (h = fma(x, w, b), k_linear_k1's step)
+// and the layout change with layer 0's input fake-quant in one pass: the
+// lift's output is formed in registers, so h is written once and never
+// read back.  Element roles as k_to_channel_major.
+template <int TT, int FQ>
+__global__ __launch_bounds__(256) void k_lift_layout(const float* x, const float* Wl, const float* bl, float* h,
+                                                     float* hc, int64_t samples, int n, int w, FakeQuant fq) {
+    constexpr int PER = TT * 64 / 256;
+    constexpr int CSTEP = 256 / TT;
+    static_assert(PER * 256 == TT * 64 && CSTEP * TT == 256, "tile size");
+    __shared__ float tile[64][TT + 1];
+    __shared__ float steps[16];
+    stage_steps(steps, fq.thr);
+    const ScaleInv inv = scale_inv(fq.scale);
+    const int cm = threadIdx.x / TT, tm = threadIdx.x % TT;
+    const int tk = threadIdx.x / 64, ck = threadIdx.x % 64;
+    const int64_t o1 = static_cast<int64_t>(cm) * n + tm, d1 = static_cast<int64_t>(CSTEP) * n;
+    const int64_t o2 = static_cast<int64_t>(tk) * w + ck, d2 = 4 * static_cast<int64_t>(w);
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, samples, n, w, tl); id += gridDim.x) {
+        const int nt = n - tl.t0 < TT ? n - tl.t0 : TT;
+        const int nc = w - tl.c0 < 64 ? w - tl.c0 : 64;
+        const bool full = nt == TT && nc == 64;
+        const int64_t cb = (tl.s * w + tl.c0) * static_cast<int64_t>(n) + tl.t0 + o1;
+        const int64_t tb = (tl.s * n + tl.t0) * static_cast<int64_t>(w) + tl.c0 + o2;
+        const int64_t xb = tl.s * static_cast<int64_t>(n) + tl.t0 + tk;
+        auto c_ok = [&](int q) { return full || (cm + CSTEP * q < nc && tm < nt); };
+        auto t_ok = [&](int q) { return full || (tk + 4 * q < nt && ck < nc); };
+        const bool col = full || ck < nc;
+        const float wv = col ? Wl[tl.c0 + ck] : 0.0f;
+        const float bv = (col && bl) ? bl[tl.c0 + ck] : 0.0f;
+        float v[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) v[q] = t_ok(q) ? x[xb + 4 * q] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            v[q] = __builtin_fmaf(v[q], wv, bv);
+            if constexpr (FQ == 1) v[q] = x2_fake_quant_inv(v[q], fq.scale, inv.inv, inv.ok, fq.zpf);
+            else if constexpr (FQ == 3) v[q] = log2_snap(v[q], fq.scale, steps);
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            if (t_ok(q)) {
+                h[tb + q * d2] = v[q];
+                tile[ck][tk + 4 * q] = v[q];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < PER; ++q)
+            if (c_ok(q)) hc[cb + q * d1] = tile[cm + CSTEP * q][tm];
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Radix-2 FFT of one channel held by one wave in LDS (fft.cpp:34-68).
 // ---------------------------------------------------------------------------
@@ -1067,6 +1122,28 @@ static void launch_channel_major_tt(float* h, float* hc, int64_t samples, int n,
         hipLaunchKernelGGL((k_to_channel_major<TT, 3>), grid, dim3(256), 0, st, h, hc, samples, n, w, fq);
     else
         hipLaunchKernelGGL((k_to_channel_major<TT, 0>), grid, dim3(256), 0, st, h, hc, samples, n, w, fq);
+}
+
+template <int TT>
+static void launch_lift_layout_tt(const float* x, const float* W, const float* b, float* h, float* hc,
+                                  int64_t samples, int n, int w, const FakeQuant& fq, hipStream_t st) {
+    const dim3 grid(grid_for(tile_count(samples, n, w, TT), 1, 8));
+    if (fq.on == 1)
+        hipLaunchKernelGGL((k_lift_layout<TT, 1>), grid, dim3(256), 0, st, x, W, b, h, hc, samples, n, w, fq);
+    else if (fq.on == 3)
+        hipLaunchKernelGGL((k_lift_layout<TT, 3>), grid, dim3(256), 0, st, x, W, b, h, hc, samples, n, w, fq);
+    else
+        hipLaunchKernelGGL((k_lift_layout<TT, 0>), grid, dim3(256), 0, st, x, W, b, h, hc, samples, n, w, fq);
+}
+
+hipError_t launch_lift_layout(const float* x, const float* W, const float* b, float* h, float* hc, int64_t samples,
+                              int n, int w, FakeQuant fq, hipStream_t st) {
+    if (samples <= 0) return hipSuccess;
+    if (small_tiles(samples, n, w))
+        launch_lift_layout_tt<8>(x, W, b, h, hc, samples, n, w, fq, st);
+    else
+        launch_lift_layout_tt<64>(x, W, b, h, hc, samples, n, w, fq, st);
+    return hipGetLastError();
 }
 
 hipError_t launch_to_channel_major(float* h, float* hc, int64_t samples, int n, int w, FakeQuant fq,

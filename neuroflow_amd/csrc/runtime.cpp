@@ -611,13 +611,21 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
         return f;
     };
 
-    LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), H, b, static_cast<int>(n_pad), static_cast<int>(n),
-                 static_cast<int>(n), rt->in_ch, w, RT_ACT_NONE};
-    if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
-    if (rt->n_layers > 0)
-        if (int rc = launch_check(launch_to_channel_major(H, HC, b, static_cast<int>(n_pad), w, in_fq(0), st),
-                                  "layout change"))
+    if (rt->in_ch == 1 && n_pad == n && rt->n_layers > 0) {
+        // The lift (one input channel) and the layout change in one pass.
+        if (int rc = launch_check(launch_lift_layout(x, rt->dw("lift.weight"), rt->dw("lift.bias"), H, HC, b,
+                                                     static_cast<int>(n), w, in_fq(0), st),
+                                  "lift + layout change"))
             return rc;
+    } else {
+        LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), H, b, static_cast<int>(n_pad), static_cast<int>(n),
+                     static_cast<int>(n), rt->in_ch, w, RT_ACT_NONE};
+        if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
+        if (rt->n_layers > 0)
+            if (int rc = launch_check(launch_to_channel_major(H, HC, b, static_cast<int>(n_pad), w, in_fq(0), st),
+                                      "layout change"))
+                return rc;
+    }
     int log2n = 0;
     while ((int64_t(1) << log2n) < n_pad) ++log2n;
     for (int i = 0; i < rt->n_layers; ++i) {
@@ -728,17 +736,26 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
     // lift.output's fake-quant (fno.cpp:852-865; the pads are zeros, which
     // every fake-quant keeps at +0).
     const int ip0 = static_cast<int>(pts0);
-    LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), padded ? P : Hb, b, ip0, ip0, ip0, rt->in_ch, w,
-                 RT_ACT_NONE};
-    if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
-    if (padded)
-        if (int rc = launch_check(launch_pad2d(P, Hb, b, H, W, Hp, Wp, w, false, st), "padding")) return rc;
-    if (rt->n_layers > 0) {
-        if (int rc = launch_check(launch_to_channel_major(Hb, HC, b, static_cast<int>(pts), w, rt->fq_lift, st),
-                                  "layout change"))
+    if (rt->in_ch == 1 && !padded && rt->n_layers > 0) {
+        // The lift (one input channel) and the layout change in one pass.
+        if (int rc = launch_check(launch_lift_layout(x, rt->dw("lift.weight"), rt->dw("lift.bias"), Hb, HC, b,
+                                                     static_cast<int>(pts), w, rt->fq_lift, st),
+                                  "lift + layout change"))
             return rc;
-    } else if (int rc = launch_check(launch_fq_act(Hb, b * pts * w, rt->fq_lift, RT_ACT_NONE, st), "lift fake-quant")) {
-        return rc;
+    } else {
+        LinArgs lift{x, rt->dw("lift.weight"), rt->dw("lift.bias"), padded ? P : Hb, b, ip0, ip0, ip0, rt->in_ch, w,
+                     RT_ACT_NONE};
+        if (int rc = launch_check(launch_linear_ref(lift, st), "lift")) return rc;
+        if (padded)
+            if (int rc = launch_check(launch_pad2d(P, Hb, b, H, W, Hp, Wp, w, false, st), "padding")) return rc;
+        if (rt->n_layers > 0) {
+            if (int rc = launch_check(launch_to_channel_major(Hb, HC, b, static_cast<int>(pts), w, rt->fq_lift, st),
+                                      "layout change"))
+                return rc;
+        } else if (int rc = launch_check(launch_fq_act(Hb, b * pts * w, rt->fq_lift, RT_ACT_NONE, st),
+                                         "lift fake-quant")) {
+            return rc;
+        }
     }
     for (int i = 0; i < rt->n_layers; ++i) {
         const LayerQuant& q = rt->lq[i];
