@@ -172,6 +172,10 @@ struct LayerTailArgs {
     int32_t zpA;
 };
 bool layer_tail_ok(const PostArgs& p, int in_features, int out_features);
+// The fp32 local linear (64 x 64, launch_linear_ref's sums) and the tail in
+// one pass, on the same conditions; W (64, 64) and b (64 or null) fp32.
+bool linear_tail_ok(const PostArgs& p, const float* W);
+hipError_t launch_linear_tail(const PostArgs& a, const float* W, const float* b, hipStream_t st);
 // The device arrays of an INT8 layer handle into a (layer.cpp): false for
 // another format.
 bool layer_int8_arrays(const nflow_layer* layer, LayerTailArgs* a, int* in_features, int* out_features);

@@ -1013,6 +1013,84 @@ __global__ __launch_bounds__(256) void k_layer_tail(LayerTailArgs la) {
     }
 }
 
+// The fp32 local-linear layer (k_linear_rows64's sums: bias, then the 64
+// products rounded and added in order) and the tail in one pass, on the
+// tail's 32-token tiles at width 64: lane j of every wave holds row j of W
+// in registers, the h tile is staged in LDS (token-major) and read back as
+// broadcasts, and the lane's eight outputs (tokens x / 64 + 4 q, channel
+// x % 64) go through the tail as k_post_rt's token-major elements.
+template <int KIND, int ACT, int FQN>
+__global__ __launch_bounds__(256) void k_linear_tail(PostArgs a, const float* Wl, const float* bl) {
+    constexpr int TT = 32, PER = TT * 64 / 256, CSTEP = 256 / TT, HS = 68;
+    __shared__ float tx1[64][TT + 1];
+    __shared__ __attribute__((aligned(16))) float th[TT * HS];
+    __shared__ float thr_x2[16], thr_next[16];
+    const int n = a.n;                  // w == 64, n % 32 == 0 (linear_tail_ok)
+    if (threadIdx.x < 15) thr_x2[threadIdx.x] = a.thr[threadIdx.x];
+    stage_steps(thr_next, a.fq_next.thr);
+    const ScaleInv inv_x2 = scale_inv(a.scale), inv_next = scale_inv(a.fq_next.scale);
+    const int cm = threadIdx.x / TT, tm = threadIdx.x % TT, tk = threadIdx.x / 64, ck = threadIdx.x % 64;
+    const int hq_t = threadIdx.x / 16, hq_c = 4 * (threadIdx.x % 16);
+    float wr[64];
+#pragma unroll
+    for (int p = 0; p < 64; p += 4) {
+        const v4f q = *reinterpret_cast<const v4f*>(Wl + ck * 64 + p);
+        wr[p] = q[0];
+        wr[p + 1] = q[1];
+        wr[p + 2] = q[2];
+        wr[p + 3] = q[3];
+    }
+    const float bj = bl ? bl[ck] : 0.0f;
+    const int64_t o1 = static_cast<int64_t>(cm) * n + tm, d1 = static_cast<int64_t>(CSTEP) * n;
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, 64, tl); id += gridDim.x) {
+        const int64_t cb = tl.s * 64 * static_cast<int64_t>(n) + tl.t0 + o1;
+        const int64_t tb = (tl.s * n + tl.t0) * 64;
+        v4f hv[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) hv[q] = *reinterpret_cast<const v4f*>(a.h + tb + (hq_t + 16 * q) * 64 + hq_c);
+        float xv[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) xv[q] = a.x1c[cb + q * d1];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) *reinterpret_cast<v4f*>(th + (hq_t + 16 * q) * HS + hq_c) = hv[q];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) tx1[cm + CSTEP * q][tm] = xv[q];
+        __syncthreads();
+        float ps[PER], pz[PER];
+        if constexpr (KIND == 2) {
+            const int64_t pb = static_cast<int64_t>(ck) * n + tl.t0 + tk;
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+                ps[q] = a.pos_scales[pb + 4 * q];
+                pz[q] = static_cast<float>(a.pos_zps[pb + 4 * q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const float* hr = th + (tk + 4 * q) * HS;
+            float acc = bj;
+#pragma unroll
+            for (int p = 0; p < 64; p += 4) {
+                const v4f hp = *reinterpret_cast<const v4f*>(hr + p);
+                acc = acc + hp[0] * wr[p];
+                acc = acc + hp[1] * wr[p + 1];
+                acc = acc + hp[2] * wr[p + 2];
+                acc = acc + hp[3] * wr[p + 3];
+            }
+            tx1[ck][tk + 4 * q] = post_element<KIND, ACT, FQN>(tx1[ck][tk + 4 * q], acc, a, inv_x2, inv_next, thr_x2,
+                                                               thr_next, KIND == 2 ? ps[q] : 0.0f,
+                                                               KIND == 2 ? pz[q] : 0.0f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < PER; ++q) a.h[tb + (tk + 4 * q) * 64 + ck] = tx1[ck][tk + 4 * q];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) a.hc[cb + q * d1] = tx1[cm + CSTEP * q][tm];
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------
 // FNO2d padding and the projection fake-quants.
 // ---------------------------------------------------------------------------
@@ -1337,6 +1415,34 @@ hipError_t launch_layer_tail(const LayerTailArgs& a, hipStream_t st) {
         case 2: launch_layer_tail_act<2>(a, grid, st); break;
         case 3: launch_layer_tail_act<3>(a, grid, st); break;
         default: launch_layer_tail_act<0>(a, grid, st); break;
+    }
+    return hipGetLastError();
+}
+
+// The fp32 local linear + tail: as layer_tail_ok, for a 64 x 64 fp32 layer
+// whose rows are read as 16-byte vectors.
+bool linear_tail_ok(const PostArgs& p, const float* W) { return layer_tail_ok(p, 64, 64) && aligned(W, 16); }
+
+template <int KIND, int ACT>
+static void launch_linear_tail_fqn(const PostArgs& a, const float* W, const float* b, unsigned grid, hipStream_t st) {
+    if (a.fq_next.on == 1) hipLaunchKernelGGL((k_linear_tail<KIND, ACT, 1>), dim3(grid), dim3(256), 0, st, a, W, b);
+    else hipLaunchKernelGGL((k_linear_tail<KIND, ACT, 0>), dim3(grid), dim3(256), 0, st, a, W, b);
+}
+
+template <int KIND>
+static void launch_linear_tail_act(const PostArgs& a, const float* W, const float* b, unsigned grid, hipStream_t st) {
+    if (a.act == RT_ACT_GELU) launch_linear_tail_fqn<KIND, RT_ACT_GELU>(a, W, b, grid, st);
+    else launch_linear_tail_fqn<KIND, RT_ACT_RELU>(a, W, b, grid, st);
+}
+
+hipError_t launch_linear_tail(const PostArgs& a, const float* W, const float* b, hipStream_t st) {
+    if (a.samples <= 0) return hipSuccess;
+    const unsigned grid = grid_for(tile_count(a.samples, a.n, a.w, 32), 1, 8);
+    switch (a.kind) {
+        case 1: launch_linear_tail_act<1>(a, W, b, grid, st); break;
+        case 2: launch_linear_tail_act<2>(a, W, b, grid, st); break;
+        case 3: launch_linear_tail_act<3>(a, W, b, grid, st); break;
+        default: launch_linear_tail_act<0>(a, W, b, grid, st); break;
     }
     return hipGetLastError();
 }

@@ -665,6 +665,14 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
             if (int rc = launch_check(launch_layer_tail(lt, st), "layer + tail")) return rc;
             continue;
         }
+        // Likewise the fp32 local linear and the tail.
+        if (!(q.int8 && rt->int8_enabled) && linear_tail_ok(pa, rt->dw("locs." + si + ".weight"))) {
+            if (int rc = launch_check(launch_linear_tail(pa, rt->dw("locs." + si + ".weight"),
+                                                         rt->dw("locs." + si + ".bias"), st),
+                                      "local linear + tail"))
+                return rc;
+            continue;
+        }
         if (q.int8 && rt->int8_enabled) {
             if (int rc = nflow_layer_forward_per_tensor(rt->int8_layers[i], M, H, X2, q.sa, q.zpa, st)) return rc;
         } else {
@@ -823,6 +831,13 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
             lt.sA = q.sa;
             lt.zpA = q.zpa;
             if (int rc = launch_check(launch_layer_tail(lt, st), "layer + tail")) return rc;
+            continue;
+        }
+        if (!(q.int8 && rt->int8_enabled) && linear_tail_ok(pa, rt->dw("locs." + si + ".weight"))) {
+            if (int rc = launch_check(launch_linear_tail(pa, rt->dw("locs." + si + ".weight"),
+                                                         rt->dw("locs." + si + ".bias"), st),
+                                      "local linear + tail"))
+                return rc;
             continue;
         }
         // Local linear (fno.cpp:906-932): fp32 as in the reference, or, after

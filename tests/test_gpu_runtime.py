@@ -89,14 +89,16 @@ def test_run_bit_exact(gpu, tmp_path, case):
         assert np.array_equal(_bits(y), _bits(ref_run(tmp_path, ir, x, case[3], case[10])))
 
 
-@pytest.mark.parametrize("kinds,relu", [(["tensor"], False), (["token", "tensor", "fp8"], True),
-                                        (["fp8", "token"], False)])
-def test_layer_tail_fused_equals_two_launches(gpu, tmp_path, kinds, relu):
-    """The width-64 INT8 layer and its tail in one launch (k_layer_tail)
-    against the two launches (k_rows64 + k_post_rt, kernel path
-    no_layer_tail) and the oracle: every x2 fake-quant kind, with and
-    without zero points on the layer input."""
-    case = (20, 1024, 1, 1, 64, 16, 3, 1, relu, kinds, True)
+@pytest.mark.parametrize("kinds,relu,int8", [(["tensor"], False, True), (["token", "tensor", "fp8"], True, True),
+                                             (["fp8", "token"], False, True), (["tensor"], False, False),
+                                             (["token", "tensor", "fp8"], True, False), (None, False, False)])
+def test_layer_tail_fused_equals_two_launches(gpu, tmp_path, kinds, relu, int8):
+    """The width-64 local-linear layer and its tail in one launch
+    (k_layer_tail for INT8, k_linear_tail for fp32) against the two
+    launches (the layer + k_post_rt, kernel path no_layer_tail) and the
+    oracle: every x2 fake-quant kind, with and without zero points on the
+    INT8 layer's input, and no fake-quant at all."""
+    case = (20, 1024, 1, 1, 64, 16, 3, 1, relu, kinds, int8)
     ncpp = load()
     ir, x, m = _model(case)
     path = tmp_path / "m.nneuroir"
@@ -109,7 +111,8 @@ def test_layer_tail_fused_equals_two_launches(gpu, tmp_path, kinds, relu):
         _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", flag, C.byref(prev)), "kernel path")
         try:
             rt = ncpp.InferenceRuntime(str(path))
-            rt.enable_int8_gemm()
+            if int8:
+                rt.enable_int8_gemm()
             y = np.zeros((x.shape[0], x.shape[1], 1), np.float32)
             rt.run(x, y)
             outs.append(y)

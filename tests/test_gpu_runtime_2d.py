@@ -46,6 +46,10 @@ CASES = [
     (2, 64, 32, 2, 1, 32, 12, 12, 2, 1, False, ["tensor", "fp8"]),
     (1, 128, 64, 1, 1, 64, 12, 12, 1, 1, False, ["fp8"]),
     (1, 256, 256, 1, 1, 64, 12, 12, 1, 1, False, ["fp8"]),
+    # 512 whole 32-point tiles at width 64: the fp32 local linear and the
+    # tail in one launch.
+    (4, 64, 64, 1, 1, 64, 12, 12, 2, 1, True, ["tensor", "fp8"]),
+    (4, 64, 64, 2, 1, 64, 12, 12, 2, 1, False, None),
     (2, 8, 8, 1, 1, 8, 8, 5, 1, 1, False, None),            # all H rows and all W/2 + 1 bins
     (1, 4, 2, 1, 1, 4, 2, 2, 0, 1, False, ["tensor"]),       # no layers
     # Output element counts that are not a multiple of 4 (the fake-quant
