@@ -107,8 +107,10 @@ const char* nflow_last_error(void);
  * the LDS-DMA GEMM), "no_wide" (0 / 1: keep K = 512 / 1024 layers off the
  * persistent GEMM), "no_rows64_queue" (0 / 1: the K = N = 64 layer with
  * its static tile deal instead of the per-CU tile queue) and
- * "no_layer_tail" (0 / 1: the FNO1d runtime's width-64 INT8 layer and its
- * tail as two launches instead of one).  The
+ * "no_layer_tail" (0 / 1: the FNO runtime's width-64 local-linear layer and
+ * its tail as two launches instead of one) and "generic_fft" (0 / 1: the
+ * FNO runtime's row FFTs of 64 .. 1024 points on the any-length kernels
+ * instead of the fixed-length ones).  The
  * environment variables NFLOW_<NAME> set the initial values, read once at
  * the library's first launch.  Process-wide; *previous (if not NULL)
  * receives the value replaced.  Unknown names return NFLOW_INVALID_ARG. */

@@ -479,6 +479,13 @@ __global__ __launch_bounds__(256) void k_lift_layout(const float* x, const float
 // ---------------------------------------------------------------------------
 // Radix-2 FFT of one channel held by one wave in LDS (fft.cpp:34-68).
 // ---------------------------------------------------------------------------
+
+// A wave's LDS buffer holds element e at slot e + e / 8: a pass's stores
+// and the next pass's loads (groups spaced 1, 8 or 64 apart) then fall on
+// distinct banks, where the unpadded layout put 4 to 8 lanes of a phase on
+// one bank.
+__device__ __forceinline__ int fft_slot(int e) { return e + (e >> 3); }
+__host__ __device__ constexpr int fft_buf_len(int n) { return n + (n >> 3); }
 __device__ __forceinline__ int bit_rev(int i, int log2n) {
     return log2n == 0 ? 0 : static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(i)) >> (32 - log2n));
 }
@@ -528,7 +535,7 @@ struct FftIo {
 template <int SRC>
 __device__ __forceinline__ float2 fft_load(const FftIo& io, int e) {
     if constexpr (SRC == 0) {
-        return io.buf[e];
+        return io.buf[fft_slot(e)];
     } else {
         const int k = bit_rev(e, io.log2n);
         if constexpr (SRC == 1) {
@@ -554,7 +561,7 @@ __device__ __forceinline__ float2 fft_load(const FftIo& io, int e) {
 template <int DST>
 __device__ __forceinline__ void fft_store(const FftIo& io, int e, float2 v) {
     if constexpr (DST == 0) {
-        io.buf[e] = v;
+        io.buf[fft_slot(e)] = v;
     } else if constexpr (DST == 1) {
         if (e < io.modes) io.dst_spec[e] = v;
     } else if constexpr (DST == 2) {
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(64 * WPB) void k_rfft_modes(SpecArgs a, int64_t nlo
     const int64_t item = lb * WPB + wid;
     if (item >= a.samples * a.w) return;
     FftIo io{};
-    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * fft_buf_len(n);
     io.tw = tw;
     io.src_real = a.hc + item * n;
     io.dst_spec = reinterpret_cast<float2*>(a.spec) + item * a.modes;
@@ -730,7 +737,7 @@ __global__ __launch_bounds__(64 * WPB) void k_irfft(SpecArgs a, const float* spe
     const int64_t item = lb * WPB + wid;
     if (item >= a.samples * a.w) return;
     FftIo io{};
-    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * fft_buf_len(n);
     io.tw = tw;
     io.src_spec = reinterpret_cast<const float2*>(spec_mixed) + item * a.modes;
     io.dst_real = a.x1c + item * n;
@@ -744,6 +751,239 @@ __global__ __launch_bounds__(64 * WPB) void k_irfft(SpecArgs a, const float* spe
         io.fill_im = f.y;
     }
     fft_run<2>(io, lane, 2);
+}
+
+// ---------------------------------------------------------------------------
+// Row transforms of a fixed length n = 2^LOG2N (64 .. 1024): the butterflies
+// of fft_pass, in the same order per element, with every index known at
+// compile time.  A wave takes R = 64 G1 / n rows at a time, so that its
+// first pass (G1 = 2^P1 elements per lane) fills all 64 lanes; it keeps
+// taking row sets until the rows run out, and loads the next set's inputs
+// before it transforms the current one.  Lane buffers in LDS hold element e
+// of a row at slot e + (e >> SL), rows STRIDE slots apart (no bank
+// conflicts at n = 256).
+// ---------------------------------------------------------------------------
+template <int LOG2N> struct RowFftPlan;
+template <> struct RowFftPlan<6> { static constexpr int P1 = 3, P2 = 3, P3 = 0, SL = 3, STRIDE = 72; };
+template <> struct RowFftPlan<7> { static constexpr int P1 = 4, P2 = 3, P3 = 0, SL = 4, STRIDE = 136; };
+template <> struct RowFftPlan<8> { static constexpr int P1 = 4, P2 = 4, P3 = 0, SL = 4, STRIDE = 272; };
+template <> struct RowFftPlan<9> { static constexpr int P1 = 3, P2 = 3, P3 = 3, SL = 3, STRIDE = 576; };
+template <> struct RowFftPlan<10> { static constexpr int P1 = 4, P2 = 3, P3 = 3, SL = 4, STRIDE = 1088; };
+
+template <int LOG2N>
+struct RowFft {
+    using PL = RowFftPlan<LOG2N>;
+    static constexpr int N = 1 << LOG2N, G1 = 1 << PL::P1, R = 64 * G1 / N;
+    static constexpr int WAVE_SLOTS = R * PL::STRIDE;
+    __device__ static __forceinline__ int slot(int row, int e) { return row * PL::STRIDE + e + (e >> PL::SL); }
+};
+
+constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v >> 1); }
+constexpr int bitrevc(int v, int bits) { return bits == 0 ? 0 : ((v & 1) << (bits - 1)) | bitrevc(v >> 1, bits - 1); }
+
+// The P stages of one group on registers (fft_pass's loop body).
+template <int P, int H0>
+__device__ __forceinline__ void row_stages(float2 (&v)[1 << P], const float2* tw, int kk) {
+    constexpr int G = 1 << P;
+#pragma unroll
+    for (int st = 0; st < P; ++st) {
+        const int span = 1 << st;
+        const int h = H0 << st;
+#pragma unroll
+        for (int e = 0; e < G; ++e) {
+            if (e & span) continue;
+            const float2 w = tw[h - 1 + kk + (e & (span - 1)) * H0];
+            const float2 t = cmul_ref(v[e + span], w);
+            const float2 u = v[e];
+            v[e] = make_float2(u.x + t.x, u.y + t.y);
+            v[e + span] = make_float2(u.x - t.x, u.y - t.y);
+        }
+    }
+}
+
+// A pass after the first: groups of 2^P elements spaced H0 apart, read from
+// and (unless LAST) written back to the wave's buffer.  FWD: groups whose
+// offset kk in their block is `modes` or more feed no kept bin and are
+// skipped; E0 (modes <= H0): only element 0 of a group feeds one, and only
+// it is kept.  LAST stores the kept bins (FWD) or the real parts times
+// 1 / n (inverse).
+template <int LOG2N, int P, int H0, bool FWD, bool E0, bool LAST>
+__device__ __forceinline__ void row_pass(float2* buf, const float2* tw, int lane, int64_t item0, int64_t items,
+                                         int modes, float inv_n, float2* spec, float* out) {
+    using F = RowFft<LOG2N>;
+    constexpr int G = 1 << P, GPR = F::N / G, TOT = F::R * GPR, LH0 = ilog2c(H0);
+#pragma unroll
+    for (int it = 0; it < (TOT + 63) / 64; ++it) {
+        const int q = it * 64 + lane;
+        if (TOT % 64 != 0 && q >= TOT) continue;
+        const int row = q / GPR, g = q % GPR;
+        const int kk = g & (H0 - 1);
+        const int base = ((g >> LH0) << (LH0 + P)) + kk;
+        if (FWD && kk >= modes) continue;
+        float2 v[G];
+#pragma unroll
+        for (int e = 0; e < G; ++e) v[e] = buf[F::slot(row, base + e * H0)];
+        row_stages<P, H0>(v, tw, kk);
+        if constexpr (!LAST) {
+            if constexpr (E0) {
+                buf[F::slot(row, base)] = v[0];
+            } else {
+#pragma unroll
+                for (int e = 0; e < G; ++e) buf[F::slot(row, base + e * H0)] = v[e];
+            }
+        } else {
+            const int64_t item = item0 + row;
+            if (item >= items) continue;
+            if constexpr (FWD) {
+                if constexpr (E0) {
+                    spec[item * modes + base] = v[0];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < G; ++e)
+                        if (base + e * H0 < modes) spec[item * modes + base + e * H0] = v[e];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < G; ++e) out[item * F::N + base + e * H0] = v[e].x * inv_n;
+            }
+        }
+    }
+}
+
+// Passes 2 (and 3) of a row set, after the first pass has filled the buffer.
+template <int LOG2N, bool FWD, bool E0>
+__device__ __forceinline__ void row_rest(float2* buf, const float2* tw, int lane, int64_t item0, int64_t items,
+                                         int modes, float inv_n, float2* spec, float* out) {
+    using PL = RowFftPlan<LOG2N>;
+    constexpr int H2 = 1 << PL::P1;
+    wave_sync();
+    if constexpr (PL::P3 == 0) {
+        row_pass<LOG2N, PL::P2, H2, FWD, E0, true>(buf, tw, lane, item0, items, modes, inv_n, spec, out);
+    } else {
+        row_pass<LOG2N, PL::P2, H2, FWD, E0, false>(buf, tw, lane, item0, items, modes, inv_n, spec, out);
+        wave_sync();
+        row_pass<LOG2N, PL::P3, (H2 << PL::P2), FWD, E0, true>(buf, tw, lane, item0, items, modes, inv_n, spec,
+                                                                out);
+    }
+    wave_sync();
+}
+
+template <int N>
+__device__ __forceinline__ const float2* stage_row_twiddles(float2* smem, const float* tw) {
+    const float2* src = reinterpret_cast<const float2*>(tw);
+    for (int i = threadIdx.x; i < N - 1; i += blockDim.x) smem[i] = src[i];
+    __syncthreads();
+    return smem;
+}
+
+// Forward transform of rows of hc (items = samples * w rows of n points),
+// bins < modes to spec (k_rfft_modes's results).  E0: modes <= 2^P1.
+template <int LOG2N, bool E0>
+__global__ __launch_bounds__(256) void k_rfft_rows_fixed(SpecArgs a, int64_t nsets) {
+    using F = RowFft<LOG2N>;
+    constexpr int N = F::N, G1 = F::G1, R = F::R, GPR1 = N / G1, LB = LOG2N - RowFftPlan<LOG2N>::P1;
+    extern __shared__ float2 fsm[];
+    const float2* tw = stage_row_twiddles<N>(fsm, a.tw_fwd);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float2* buf = fsm + N + wid * F::WAVE_SLOTS;
+    const int64_t items = a.samples * a.w;
+    // First pass: lane = (row, group g); element e of the group is input
+    // bitrev(g G1 + e) = bitrev_P1(e) 2^LB + bitrev_LB(g).
+    const int row1 = lane / GPR1, g1 = lane % GPR1;
+    const int rb = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(g1)) >> (32 - LB));
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid, nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    float cur[G1];
+    auto load = [&](int64_t set, float (&d)[G1]) {
+        const int64_t item = set * R + row1;
+        if (item < items) {
+            const float* src = a.hc + item * N + rb;
+#pragma unroll
+            for (int e = 0; e < G1; ++e) d[e] = src[bitrevc(e, RowFftPlan<LOG2N>::P1) << LB];
+        } else {
+#pragma unroll
+            for (int e = 0; e < G1; ++e) d[e] = 0.0f;     // a row past the end: transformed, never stored
+        }
+    };
+    int64_t set = wave;
+    if (set < nsets) load(set, cur);
+    for (; set < nsets; set += nwaves) {
+        float nxt[G1];
+        if (set + nwaves < nsets) load(set + nwaves, nxt);
+        float2 v[G1];
+#pragma unroll
+        for (int e = 0; e < G1; ++e) v[e] = make_float2(cur[e], 0.0f);
+        row_stages<RowFftPlan<LOG2N>::P1, 1>(v, tw, 0);
+#pragma unroll
+        for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
+        row_rest<LOG2N, true, E0>(buf, tw, lane, set * R, items, a.modes, 0.0f, reinterpret_cast<float2*>(a.spec),
+                                  nullptr);
+#pragma unroll
+        for (int e = 0; e < G1; ++e) cur[e] = nxt[e];
+    }
+}
+
+// Inverse transform (k_irfft's results): bins of row item from its `modes`
+// mixed bins, bins modes .. n/2 the item's fill value, bins above n/2 the
+// conjugates of those below; real parts times 1 / n to x1c.
+template <int LOG2N>
+__global__ __launch_bounds__(256) void k_irfft_rows_fixed(SpecArgs a, const float* spec_mixed, int64_t nsets) {
+    using F = RowFft<LOG2N>;
+    constexpr int N = F::N, G1 = F::G1, R = F::R, GPR1 = N / G1, LB = LOG2N - RowFftPlan<LOG2N>::P1;
+    extern __shared__ float2 fsm[];
+    const float2* tw = stage_row_twiddles<N>(fsm, a.tw_inv);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float2* buf = fsm + N + wid * F::WAVE_SLOTS;
+    const int64_t items = a.samples * a.w;
+    const int modes = a.modes;
+    const int row1 = lane / GPR1, g1 = lane % GPR1;
+    const int rb = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(g1)) >> (32 - LB));
+    // Which of the lane's elements are mixed bins (bit e: bin k < modes, or
+    // its mirror n - k < modes above n / 2), fixed for the whole launch.
+    uint32_t mixed = 0, mirror = 0;
+#pragma unroll
+    for (int e = 0; e < G1; ++e) {
+        const int k = (bitrevc(e, RowFftPlan<LOG2N>::P1) << LB) + rb;
+        if (k <= N / 2 ? k < modes : N - k < modes) mixed |= 1u << e;
+        if (k > N / 2) mirror |= 1u << e;
+    }
+    const float2* spec = reinterpret_cast<const float2*>(spec_mixed);
+    const bool fill_pow2 = (a.fill_period & (a.fill_period - 1)) == 0;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid, nwaves = static_cast<int64_t>(gridDim.x) * 4;
+    float2 cur[G1];
+    auto load = [&](int64_t set, float2 (&d)[G1]) {
+        const int64_t item = set * R + row1;
+        if (item >= items) {
+#pragma unroll
+            for (int e = 0; e < G1; ++e) d[e] = make_float2(0.0f, 0.0f);   // transformed, never stored
+            return;
+        }
+        float2 f = make_float2(0.0f, 0.0f);
+        if (a.fill) f = a.fill[fill_pow2 ? (item & (a.fill_period - 1)) : item % a.fill_period];
+        const float2* src = spec + item * modes;
+#pragma unroll
+        for (int e = 0; e < G1; ++e) {
+            const int k = (bitrevc(e, RowFftPlan<LOG2N>::P1) << LB) + rb;
+            const bool up = (mirror >> e) & 1u;
+            float2 v = f;
+            if ((mixed >> e) & 1u) v = src[up ? N - k : k];
+            d[e] = up ? make_float2(v.x, -v.y) : v;
+        }
+    };
+    int64_t set = wave;
+    if (set < nsets) load(set, cur);
+    for (; set < nsets; set += nwaves) {
+        float2 nxt[G1];
+        if (set + nwaves < nsets) load(set + nwaves, nxt);
+        float2 v[G1];
+#pragma unroll
+        for (int e = 0; e < G1; ++e) v[e] = cur[e];
+        row_stages<RowFftPlan<LOG2N>::P1, 1>(v, tw, 0);
+#pragma unroll
+        for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
+        row_rest<LOG2N, false, false>(buf, tw, lane, set * R, items, modes, a.inv_n, nullptr, a.x1c);
+#pragma unroll
+        for (int e = 0; e < G1; ++e) cur[e] = nxt[e];
+    }
 }
 
 // Column FFT (fft.cpp:48-68 down column j of a plane, fft.cpp:111-122 /
@@ -762,7 +1002,7 @@ __global__ __launch_bounds__(64 * WPB) void k_cfft_cols(ColArgs a, int64_t nlogi
     const int j = static_cast<int>(item % a.mw);
     const int in_rows = INV ? a.mh : a.h, out_rows = INV ? a.h : a.mh;
     FftIo io{};
-    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * n;
+    io.buf = fsm + (TWL ? n : 0) + static_cast<int64_t>(wid) * fft_buf_len(n);
     io.tw = tw;
     io.src_spec = reinterpret_cast<const float2*>(a.in) + plane * in_rows * a.mw + j;
     io.src_stride = a.mw;
@@ -1249,13 +1489,59 @@ static FftLaunch fft_launch(int64_t items, int n) {
     const int wpb = f.small ? 4 : 1;
     f.nlogical = (items + wpb - 1) / wpb;
     f.grid = static_cast<unsigned>(8 * ((f.nlogical + 7) / 8));
-    f.lds = (static_cast<size_t>(wpb) * n + (f.small ? n : 0)) * sizeof(float2);
+    f.lds = (static_cast<size_t>(wpb) * fft_buf_len(n) + (f.small ? n : 0)) * sizeof(float2);
     return f;
+}
+
+// The fixed-length row kernels: lengths 64 .. 1024, a persistent grid of at
+// most eight blocks of four waves per CU, each wave taking R rows at a time.
+template <int LOG2N>
+static bool row_fixed_launch(int64_t items, unsigned& grid, int64_t& nsets, size_t& lds) {
+    if (path_flag(kernel_path().generic_fft)) return false;
+    using F = RowFft<LOG2N>;
+    nsets = (items + F::R - 1) / F::R;
+    const int64_t blocks = (nsets + 3) / 4, cap = 8 * static_cast<int64_t>(num_cus());
+    grid = static_cast<unsigned>(blocks < cap ? blocks : cap);
+    lds = (static_cast<size_t>(F::N) + 4 * static_cast<size_t>(F::WAVE_SLOTS)) * sizeof(float2);
+    return true;
+}
+
+template <int LOG2N>
+static bool launch_rfft_fixed(const SpecArgs& a, int64_t items, hipStream_t st) {
+    unsigned grid;
+    int64_t nsets;
+    size_t lds;
+    if (!row_fixed_launch<LOG2N>(items, grid, nsets, lds)) return false;
+    if (a.modes <= RowFft<LOG2N>::G1)
+        hipLaunchKernelGGL((k_rfft_rows_fixed<LOG2N, true>), dim3(grid), dim3(256), lds, st, a, nsets);
+    else
+        hipLaunchKernelGGL((k_rfft_rows_fixed<LOG2N, false>), dim3(grid), dim3(256), lds, st, a, nsets);
+    return true;
+}
+
+template <int LOG2N>
+static bool launch_irfft_fixed(const SpecArgs& a, int64_t items, hipStream_t st) {
+    unsigned grid;
+    int64_t nsets;
+    size_t lds;
+    if (!row_fixed_launch<LOG2N>(items, grid, nsets, lds)) return false;
+    hipLaunchKernelGGL((k_irfft_rows_fixed<LOG2N>), dim3(grid), dim3(256), lds, st, a, a.spec_mixed, nsets);
+    return true;
 }
 
 hipError_t launch_rfft_rows(const SpecArgs& a, hipStream_t st) {
     const int64_t items = a.samples * a.w;
     if (items <= 0) return hipSuccess;
+    bool fixed = false;
+    switch (a.log2n) {
+        case 6: fixed = launch_rfft_fixed<6>(a, items, st); break;
+        case 7: fixed = launch_rfft_fixed<7>(a, items, st); break;
+        case 8: fixed = launch_rfft_fixed<8>(a, items, st); break;
+        case 9: fixed = launch_rfft_fixed<9>(a, items, st); break;
+        case 10: fixed = launch_rfft_fixed<10>(a, items, st); break;
+        default: break;
+    }
+    if (fixed) return hipGetLastError();
     const FftLaunch f = fft_launch(items, a.n);
     if (f.small)
         hipLaunchKernelGGL((k_rfft_modes<4, true>), dim3(f.grid), dim3(256), f.lds, st, a, f.nlogical);
@@ -1275,6 +1561,16 @@ hipError_t launch_spec_mix(const SpecArgs& a, hipStream_t st) {
 hipError_t launch_irfft_rows(const SpecArgs& a, hipStream_t st) {
     const int64_t items = a.samples * a.w;
     if (items <= 0) return hipSuccess;
+    bool fixed = false;
+    switch (a.log2n) {
+        case 6: fixed = launch_irfft_fixed<6>(a, items, st); break;
+        case 7: fixed = launch_irfft_fixed<7>(a, items, st); break;
+        case 8: fixed = launch_irfft_fixed<8>(a, items, st); break;
+        case 9: fixed = launch_irfft_fixed<9>(a, items, st); break;
+        case 10: fixed = launch_irfft_fixed<10>(a, items, st); break;
+        default: break;
+    }
+    if (fixed) return hipGetLastError();
     const FftLaunch f = fft_launch(items, a.n);
     if (f.small)
         hipLaunchKernelGGL((k_irfft<4, true>), dim3(f.grid), dim3(256), f.lds, st, a, a.spec_mixed, f.nlogical);

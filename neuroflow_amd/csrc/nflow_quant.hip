@@ -422,6 +422,7 @@ KernelPath& kernel_path() {
         p->no_wide.store(env_int("NFLOW_NO_WIDE"));
         p->no_rows64_queue.store(env_int("NFLOW_NO_ROWS64_QUEUE"));
         p->no_layer_tail.store(env_int("NFLOW_NO_LAYER_TAIL"));
+        p->generic_fft.store(env_int("NFLOW_GENERIC_FFT"));
         return p;
     }();
     return *k;
@@ -583,7 +584,8 @@ int nflow_debug_set_kernel_path(const char* name, int value, int* previous) {
                         : n == "gemm_mfma" ? &k.gemm_mfma
                         : n == "no_wide" ? &k.no_wide
                         : n == "no_rows64_queue" ? &k.no_rows64_queue
-                        : n == "no_layer_tail" ? &k.no_layer_tail : nullptr;
+                        : n == "no_layer_tail" ? &k.no_layer_tail
+                        : n == "generic_fft" ? &k.generic_fft : nullptr;
     if (!f) return set_error(NFLOW_INVALID_ARG, "debug_set_kernel_path: unknown name " + n);
     const int old = f->exchange(value, std::memory_order_relaxed);
     if (previous) *previous = old;

@@ -61,6 +61,17 @@ CASES = [
     # A batch whose lift (one input channel, width 64) takes several passes
     # of the grid: each thread's columns stay fixed from pass to pass.
     (160, 1024, 1, 1, 64, 16, 1, 1, False, ["tensor"], True),
+    # The fixed-length row FFTs (64 .. 1024 points): modes up to the first
+    # pass's group size (only element 0 of later groups kept) and above it,
+    # and row counts that leave the last row set part-filled (15 rows).
+    (3, 512, 1, 1, 16, 8, 2, 1, False, ["tensor"], False),
+    (2, 512, 2, 1, 12, 20, 2, 1, True, None, False),
+    (4, 128, 1, 2, 16, 24, 2, 1, False, ["fp8"], False),
+    (3, 128, 1, 1, 5, 9, 1, 1, False, None, False),
+    (3, 256, 1, 1, 5, 40, 2, 1, True, ["tensor"], False),
+    (1, 1024, 1, 1, 8, 100, 1, 1, False, None, False),
+    (3, 64, 1, 1, 5, 4, 1, 1, False, None, False),
+    (3, 64, 1, 1, 5, 33, 1, 1, True, None, False),
 ]
 
 
@@ -120,6 +131,30 @@ def test_layer_tail_fused_equals_two_launches(gpu, tmp_path, kinds, relu, int8):
             _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", prev.value, None), "kernel path")
     for y in outs:
         assert np.array_equal(_bits(y), _bits(want)), int((_bits(y) != _bits(want)).sum())
+
+
+@pytest.mark.parametrize("case", [(3, 256, 1, 1, 16, 12, 2, 1, False, ["tensor"], False),
+                                  (2, 1024, 1, 1, 16, 16, 2, 1, True, None, False),
+                                  (3, 256, 1, 1, 5, 40, 1, 1, False, None, False)], ids=_ids)
+def test_fixed_length_ffts_equal_generic(gpu, tmp_path, case):
+    """The fixed-length row FFT kernels against the any-length ones (kernel
+    path generic_fft) and the oracle."""
+    ncpp = load()
+    ir, x, m = _model(case)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    want = OF.forward(m, x)
+    L = _lib.lib()
+    for flag in (0, 1):
+        prev = C.c_int(0)
+        _lib.check(L.nflow_debug_set_kernel_path(b"generic_fft", flag, C.byref(prev)), "kernel path")
+        try:
+            rt = ncpp.InferenceRuntime(str(path))
+            y = np.zeros((x.shape[0], x.shape[1], case[3]), np.float32)
+            rt.run(x, y)
+        finally:
+            _lib.check(L.nflow_debug_set_kernel_path(b"generic_fft", prev.value, None), "kernel path")
+        assert np.array_equal(_bits(y), _bits(want)), (flag, int((_bits(y) != _bits(want)).sum()))
 
 
 def test_dispatch_matches_the_reference_decision(gpu, tmp_path):

@@ -50,6 +50,10 @@ CASES = [
     # tail in one launch.
     (4, 64, 64, 1, 1, 64, 12, 12, 2, 1, True, ["tensor", "fp8"]),
     (4, 64, 64, 2, 1, 64, 12, 12, 2, 1, False, None),
+    # Row lengths 128 and 512 on the fixed-length row FFTs, 12 rows (a
+    # part-filled row set of 8 at 128 points).
+    (1, 4, 128, 1, 1, 3, 3, 20, 1, 1, False, ["tensor"]),
+    (2, 4, 512, 1, 1, 4, 2, 6, 1, 1, True, None),
     (2, 8, 8, 1, 1, 8, 8, 5, 1, 1, False, None),            # all H rows and all W/2 + 1 bins
     (1, 4, 2, 1, 1, 4, 2, 2, 0, 1, False, ["tensor"]),       # no layers
     # Output element counts that are not a multiple of 4 (the fake-quant
