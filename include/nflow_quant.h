@@ -109,8 +109,8 @@ const char* nflow_last_error(void);
  * its static tile deal instead of the per-CU tile queue) and
  * "no_layer_tail" (0 / 1: the FNO runtime's width-64 local-linear layer and
  * its tail as two launches instead of one) and "generic_fft" (0 / 1: the
- * FNO runtime's row FFTs of 64 .. 1024 points on the any-length kernels
- * instead of the fixed-length ones).  The
+ * FNO runtime's row FFTs of 64 .. 1024 points and its channel mix of up to
+ * 64 channels on the any-size kernels instead of the fixed-size ones).  The
  * environment variables NFLOW_<NAME> set the initial values, read once at
  * the library's first launch.  Process-wide; *previous (if not NULL)
  * receives the value replaced.  Unknown names return NFLOW_INVALID_ARG. */

@@ -724,6 +724,59 @@ __global__ __launch_bounds__(256) void k_spec_mix(SpecArgs a, const float* mix_r
     reinterpret_cast<float2*>(spec_out)[(s * w + wo) * modes + m] = make_float2(sr, si);
 }
 
+// The same mix for w <= 64 with the operands staged in LDS first: a block
+// takes mode m (blockIdx.y) for four samples (one per wave), loads the
+// mode's w x w weights and the four samples' w input bins with all of its
+// loads in flight at once, then sums from LDS in the same order and fused
+// forms as k_spec_mix (lane = output channel).
+// W: the channel count when fixed at compile time (64), else 0.
+template <int W>
+__global__ __launch_bounds__(256) void k_spec_mix_lds(SpecArgs a, const float* mix_r, const float* mix_i,
+                                                      float* spec_out) {
+    __shared__ float wr_s[64 * 64], wi_s[64 * 64];
+    __shared__ float2 h_s[4][64];
+    const int m = blockIdx.y;
+    const int w = W ? W : a.w, modes = a.modes, ww = w * w;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int64_t s0 = static_cast<int64_t>(blockIdx.x) * 4;
+    const float* Wr = mix_r + static_cast<int64_t>(m) * ww;
+    const float* Wi = mix_i + static_cast<int64_t>(m) * ww;
+    // Every load of the stage is issued before the first is waited for.
+    float vr[16], vi[16];
+    float2 hin = make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < ww) {
+            vr[j] = Wr[i];
+            vi[j] = Wi[i];
+        }
+    }
+    const int64_t s = s0 + wid;
+    const bool live = lane < w && s < a.samples;
+    if (live) hin = reinterpret_cast<const float2*>(a.spec)[(s * w + lane) * modes + m];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < ww) {
+            wr_s[i] = vr[j];
+            wi_s[i] = vi[j];
+        }
+    }
+    h_s[wid][lane] = hin;
+    __syncthreads();
+    if (!live) return;
+    float sr = 0.0f, si = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < w; ++k) {
+        const float2 hv = h_s[wid][k];
+        const float wr = wr_s[k * w + lane], wim = wi_s[k * w + lane];
+        sr = sr + __builtin_fmaf(-wim, hv.y, hv.x * wr);
+        si = si + __builtin_fmaf(wr, hv.y, hv.x * wim);
+    }
+    reinterpret_cast<float2*>(spec_out)[(s * w + lane) * modes + m] = make_float2(sr, si);
+}
+
 // Inverse FFT (fft.cpp:86-100) of output channel wo of sample s from the
 // mixed spectrum, written channel-major to x1c.
 template <int WPB, bool TWL>
@@ -802,14 +855,13 @@ __device__ __forceinline__ void row_stages(float2 (&v)[1 << P], const float2* tw
 }
 
 // A pass after the first: groups of 2^P elements spaced H0 apart, read from
-// and (unless LAST) written back to the wave's buffer.  FWD: groups whose
-// offset kk in their block is `modes` or more feed no kept bin and are
-// skipped; E0 (modes <= H0): only element 0 of a group feeds one, and only
-// it is kept.  LAST stores the kept bins (FWD) or the real parts times
-// 1 / n (inverse).
-template <int LOG2N, int P, int H0, bool FWD, bool E0, bool LAST>
-__device__ __forceinline__ void row_pass(float2* buf, const float2* tw, int lane, int64_t item0, int64_t items,
-                                         int modes, float inv_n, float2* spec, float* out) {
+// and (unless LAST) written back to the wave's buffer.  PRUNE: groups whose
+// offset kk in their block is io.keep or more feed no kept output and are
+// skipped; E0 (io.keep <= H0): only element 0 of a group feeds one, and
+// only it is kept.  LAST hands the kept outputs (position < io.keep when
+// PRUNE) of item item0 + row to io.store.
+template <int LOG2N, int P, int H0, bool PRUNE, bool E0, bool LAST, class IO>
+__device__ __forceinline__ void row_pass(float2* buf, const float2* tw, int lane, int64_t item0, const IO& io) {
     using F = RowFft<LOG2N>;
     constexpr int G = 1 << P, GPR = F::N / G, TOT = F::R * GPR, LH0 = ilog2c(H0);
 #pragma unroll
@@ -819,7 +871,7 @@ __device__ __forceinline__ void row_pass(float2* buf, const float2* tw, int lane
         const int row = q / GPR, g = q % GPR;
         const int kk = g & (H0 - 1);
         const int base = ((g >> LH0) << (LH0 + P)) + kk;
-        if (FWD && kk >= modes) continue;
+        if (PRUNE && kk >= io.keep) continue;
         float2 v[G];
 #pragma unroll
         for (int e = 0; e < G; ++e) v[e] = buf[F::slot(row, base + e * H0)];
@@ -833,37 +885,31 @@ __device__ __forceinline__ void row_pass(float2* buf, const float2* tw, int lane
             }
         } else {
             const int64_t item = item0 + row;
-            if (item >= items) continue;
-            if constexpr (FWD) {
-                if constexpr (E0) {
-                    spec[item * modes + base] = v[0];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < G; ++e)
-                        if (base + e * H0 < modes) spec[item * modes + base + e * H0] = v[e];
-                }
+            if (item >= io.items) continue;
+            const int64_t ob = io.out_base(item);
+            if constexpr (E0) {
+                io.store(ob, base, v[0]);
             } else {
 #pragma unroll
-                for (int e = 0; e < G; ++e) out[item * F::N + base + e * H0] = v[e].x * inv_n;
+                for (int e = 0; e < G; ++e)
+                    if (!PRUNE || base + e * H0 < io.keep) io.store(ob, base + e * H0, v[e]);
             }
         }
     }
 }
 
 // Passes 2 (and 3) of a row set, after the first pass has filled the buffer.
-template <int LOG2N, bool FWD, bool E0>
-__device__ __forceinline__ void row_rest(float2* buf, const float2* tw, int lane, int64_t item0, int64_t items,
-                                         int modes, float inv_n, float2* spec, float* out) {
+template <int LOG2N, bool PRUNE, bool E0, class IO>
+__device__ __forceinline__ void row_rest(float2* buf, const float2* tw, int lane, int64_t item0, const IO& io) {
     using PL = RowFftPlan<LOG2N>;
     constexpr int H2 = 1 << PL::P1;
     wave_sync();
     if constexpr (PL::P3 == 0) {
-        row_pass<LOG2N, PL::P2, H2, FWD, E0, true>(buf, tw, lane, item0, items, modes, inv_n, spec, out);
+        row_pass<LOG2N, PL::P2, H2, PRUNE, E0, true>(buf, tw, lane, item0, io);
     } else {
-        row_pass<LOG2N, PL::P2, H2, FWD, E0, false>(buf, tw, lane, item0, items, modes, inv_n, spec, out);
+        row_pass<LOG2N, PL::P2, H2, PRUNE, E0, false>(buf, tw, lane, item0, io);
         wave_sync();
-        row_pass<LOG2N, PL::P3, (H2 << PL::P2), FWD, E0, true>(buf, tw, lane, item0, items, modes, inv_n, spec,
-                                                                out);
+        row_pass<LOG2N, PL::P3, (H2 << PL::P2), PRUNE, E0, true>(buf, tw, lane, item0, io);
     }
     wave_sync();
 }
@@ -876,115 +922,219 @@ __device__ __forceinline__ const float2* stage_row_twiddles(float2* smem, const 
     return smem;
 }
 
-// Forward transform of rows of hc (items = samples * w rows of n points),
-// bins < modes to spec (k_rfft_modes's results).  E0: modes <= 2^P1.
-template <int LOG2N, bool E0>
-__global__ __launch_bounds__(256) void k_rfft_rows_fixed(SpecArgs a, int64_t nsets) {
-    using F = RowFft<LOG2N>;
-    constexpr int N = F::N, G1 = F::G1, R = F::R, GPR1 = N / G1, LB = LOG2N - RowFftPlan<LOG2N>::P1;
-    extern __shared__ float2 fsm[];
-    const float2* tw = stage_row_twiddles<N>(fsm, a.tw_fwd);
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    float2* buf = fsm + N + wid * F::WAVE_SLOTS;
-    const int64_t items = a.samples * a.w;
-    // First pass: lane = (row, group g); element e of the group is input
-    // bitrev(g G1 + e) = bitrev_P1(e) 2^LB + bitrev_LB(g).
-    const int row1 = lane / GPR1, g1 = lane % GPR1;
-    const int rb = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(g1)) >> (32 - LB));
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid, nwaves = static_cast<int64_t>(gridDim.x) * 4;
-    float cur[G1];
-    auto load = [&](int64_t set, float (&d)[G1]) {
-        const int64_t item = set * R + row1;
-        if (item < items) {
-            const float* src = a.hc + item * N + rb;
-#pragma unroll
-            for (int e = 0; e < G1; ++e) d[e] = src[bitrevc(e, RowFftPlan<LOG2N>::P1) << LB];
-        } else {
-#pragma unroll
-            for (int e = 0; e < G1; ++e) d[e] = 0.0f;     // a row past the end: transformed, never stored
-        }
-    };
-    int64_t set = wave;
-    if (set < nsets) load(set, cur);
-    for (; set < nsets; set += nwaves) {
-        float nxt[G1];
-        if (set + nwaves < nsets) load(set + nwaves, nxt);
-        float2 v[G1];
-#pragma unroll
-        for (int e = 0; e < G1; ++e) v[e] = make_float2(cur[e], 0.0f);
-        row_stages<RowFftPlan<LOG2N>::P1, 1>(v, tw, 0);
-#pragma unroll
-        for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
-        row_rest<LOG2N, true, E0>(buf, tw, lane, set * R, items, a.modes, 0.0f, reinterpret_cast<float2*>(a.spec),
-                                  nullptr);
-#pragma unroll
-        for (int e = 0; e < G1; ++e) cur[e] = nxt[e];
+// The persistent row-set loop: a wave loads the inputs of its next set into
+// one of two register buffers while it transforms the set held in the other
+// (the two alternate, so no copy between them).
+template <typename Buf, typename Load, typename Run>
+__device__ __forceinline__ void row_sets(int64_t first, int64_t stride, int64_t nsets, Buf& b0, Buf& b1,
+                                         const Load& load, const Run& run) {
+    int64_t set = first;
+    if (set < nsets) load(set, b0);
+    while (set < nsets) {
+        if (set + stride < nsets) load(set + stride, b1);
+        run(set, b0);
+        set += stride;
+        if (set >= nsets) break;
+        if (set + stride < nsets) load(set + stride, b0);
+        run(set, b1);
+        set += stride;
     }
 }
 
-// Inverse transform (k_irfft's results): bins of row item from its `modes`
-// mixed bins, bins modes .. n/2 the item's fill value, bins above n/2 the
-// conjugates of those below; real parts times 1 / n to x1c.
-template <int LOG2N>
-__global__ __launch_bounds__(256) void k_irfft_rows_fixed(SpecArgs a, const float* spec_mixed, int64_t nsets) {
+// The fixed-length transform of `items` sequences, R per wave at a time.
+// IO supplies the sequences and takes the results: IO::Lane, the lane's
+// constants (from its first-pass row and bit-reversed group index);
+// IO::In, one set's prefetched inputs; load(lane, set, item, in);
+// first(lane, in, v), the first pass's G1 inputs (element e = input
+// bitrev(g G1 + e) = bitrev_P1(e) 2^LB + bitrev_LB(g)); out_base(item) and
+// store(base, position, value) for the kept outputs.
+template <int LOG2N, bool PRUNE, bool E0, class IO>
+__global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
     using F = RowFft<LOG2N>;
     constexpr int N = F::N, G1 = F::G1, R = F::R, GPR1 = N / G1, LB = LOG2N - RowFftPlan<LOG2N>::P1;
     extern __shared__ float2 fsm[];
-    const float2* tw = stage_row_twiddles<N>(fsm, a.tw_inv);
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const float2* tw = stage_row_twiddles<N>(fsm, io.tw);
+    const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     float2* buf = fsm + N + wid * F::WAVE_SLOTS;
-    const int64_t items = a.samples * a.w;
-    const int modes = a.modes;
     const int row1 = lane / GPR1, g1 = lane % GPR1;
     const int rb = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(g1)) >> (32 - LB));
-    // Which of the lane's elements are mixed bins (bit e: bin k < modes, or
-    // its mirror n - k < modes above n / 2), fixed for the whole launch.
-    uint32_t mixed = 0, mirror = 0;
-#pragma unroll
-    for (int e = 0; e < G1; ++e) {
-        const int k = (bitrevc(e, RowFftPlan<LOG2N>::P1) << LB) + rb;
-        if (k <= N / 2 ? k < modes : N - k < modes) mixed |= 1u << e;
-        if (k > N / 2) mirror |= 1u << e;
-    }
-    const float2* spec = reinterpret_cast<const float2*>(spec_mixed);
-    const bool fill_pow2 = (a.fill_period & (a.fill_period - 1)) == 0;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + wid, nwaves = static_cast<int64_t>(gridDim.x) * 4;
-    float2 cur[G1];
-    auto load = [&](int64_t set, float2 (&d)[G1]) {
-        const int64_t item = set * R + row1;
-        if (item >= items) {
-#pragma unroll
-            for (int e = 0; e < G1; ++e) d[e] = make_float2(0.0f, 0.0f);   // transformed, never stored
-            return;
-        }
-        float2 f = make_float2(0.0f, 0.0f);
-        if (a.fill) f = a.fill[fill_pow2 ? (item & (a.fill_period - 1)) : item % a.fill_period];
-        const float2* src = spec + item * modes;
-#pragma unroll
-        for (int e = 0; e < G1; ++e) {
-            const int k = (bitrevc(e, RowFftPlan<LOG2N>::P1) << LB) + rb;
-            const bool up = (mirror >> e) & 1u;
-            float2 v = f;
-            if ((mixed >> e) & 1u) v = src[up ? N - k : k];
-            d[e] = up ? make_float2(v.x, -v.y) : v;
-        }
-    };
-    int64_t set = wave;
-    if (set < nsets) load(set, cur);
-    for (; set < nsets; set += nwaves) {
-        float2 nxt[G1];
-        if (set + nwaves < nsets) load(set + nwaves, nxt);
+    const typename IO::Lane ln = io.lane_setup(row1, rb);
+    using In = typename IO::In;
+    auto load = [&](int64_t set, In& d) { io.load(ln, set, set * R + row1, d); };
+    auto run = [&](int64_t set, const In& d) {
         float2 v[G1];
-#pragma unroll
-        for (int e = 0; e < G1; ++e) v[e] = cur[e];
+        io.first(ln, d, v);
         row_stages<RowFftPlan<LOG2N>::P1, 1>(v, tw, 0);
 #pragma unroll
         for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
-        row_rest<LOG2N, false, false>(buf, tw, lane, set * R, items, modes, a.inv_n, nullptr, a.x1c);
-#pragma unroll
-        for (int e = 0; e < G1; ++e) cur[e] = nxt[e];
-    }
+        row_rest<LOG2N, PRUNE, E0>(buf, tw, lane, set * R, io);
+    };
+    In b0{}, b1{};
+    row_sets(static_cast<int64_t>(blockIdx.x) * 4 + wid, static_cast<int64_t>(gridDim.x) * 4, nsets, b0, b1, load,
+             run);
 }
+
+template <int LOG2N> struct FftConsts {
+    static constexpr int N = 1 << LOG2N, P1 = RowFftPlan<LOG2N>::P1, G1 = 1 << P1, LB = LOG2N - P1;
+    __device__ static __forceinline__ int bin(int rb, int e) { return (bitrevc(e, P1) << LB) + rb; }
+};
+
+// Row FFTs of hc (k_rfft_modes's results): real rows of n points, bins
+// < keep (= modes) to spec.
+template <int LOG2N>
+struct RowFwdIO {
+    using C = FftConsts<LOG2N>;
+    const float* hc;
+    float2* spec;
+    const float* tw;
+    int64_t items;
+    int keep;
+    struct Lane { int rb; };
+    struct In { float v[C::G1]; };
+    __device__ Lane lane_setup(int, int rb) const { return Lane{rb}; }
+    __device__ void load(const Lane& ln, int64_t, int64_t item, In& d) const {
+        if (item < items) {
+            const float* src = hc + item * C::N + ln.rb;
+#pragma unroll
+            for (int e = 0; e < C::G1; ++e) d.v[e] = src[bitrevc(e, C::P1) << C::LB];
+        } else {
+#pragma unroll
+            for (int e = 0; e < C::G1; ++e) d.v[e] = 0.0f;    // a row past the end: transformed, never stored
+        }
+    }
+    __device__ void first(const Lane&, const In& d, float2 (&v)[C::G1]) const {
+#pragma unroll
+        for (int e = 0; e < C::G1; ++e) v[e] = make_float2(d.v[e], 0.0f);
+    }
+    __device__ int64_t out_base(int64_t item) const { return item * keep; }
+    __device__ void store(int64_t ob, int pos, float2 v) const { spec[ob + pos] = v; }
+};
+
+// Inverse row FFTs (k_irfft's results): the bins of row item are its
+// `modes` mixed bins, bins modes .. n/2 the item's fill value, bins above
+// n/2 the conjugates of those below; real parts times 1 / n to x1c.  With
+// FEW (modes <= 2^LB) only a lane's elements 0 and G1 - 1 can be mixed bins.
+template <int LOG2N, bool FEW>
+struct RowInvIO {
+    using C = FftConsts<LOG2N>;
+    static constexpr int G1 = C::G1;
+    const float2* spec;
+    float* out;
+    const float2* fill;
+    const float* tw;
+    int64_t items;
+    int keep;              // unused (nothing pruned)
+    int modes;
+    int fill_period;
+    float inv_n;
+    static constexpr int R = RowFft<LOG2N>::R;
+    // The lane's mixed elements (bit e) and the byte offsets of their bins
+    // in the set's mixed bins.
+    struct Lane { uint32_t off[G1]; uint32_t mixed; int rb; };
+    struct In { float2 v[FEW ? 2 : G1]; float2 f; };
+    __device__ Lane lane_setup(int row1, int rb) const {
+        Lane ln{};
+        ln.rb = rb;
+#pragma unroll
+        for (int e = 0; e < G1; ++e) {
+            const int k = C::bin(rb, e);
+            const bool up = k > C::N / 2;
+            const bool mx = up ? C::N - k < modes : k < modes;
+            ln.mixed |= mx ? 1u << e : 0u;
+            ln.off[e] = static_cast<uint32_t>(row1 * modes + (mx ? (up ? C::N - k : k) : 0)) * 8u;
+        }
+        return ln;
+    }
+    __device__ void load(const Lane& ln, int64_t set, int64_t item, In& d) const {
+        d.f = make_float2(0.0f, 0.0f);
+        if (item >= items) return;    // a row past the end: transformed, never stored
+        if (fill) {
+            const bool pow2 = (fill_period & (fill_period - 1)) == 0;
+            d.f = fill[pow2 ? (item & (fill_period - 1)) : item % fill_period];
+        }
+        const char* src = reinterpret_cast<const char*>(spec + set * R * modes);
+        if constexpr (FEW) {
+            if (ln.mixed & 1u) d.v[0] = *reinterpret_cast<const float2*>(src + ln.off[0]);
+            if ((ln.mixed >> (G1 - 1)) & 1u) d.v[1] = *reinterpret_cast<const float2*>(src + ln.off[G1 - 1]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < G1; ++e)
+                if ((ln.mixed >> e) & 1u) d.v[e] = *reinterpret_cast<const float2*>(src + ln.off[e]);
+        }
+    }
+    __device__ void first(const Lane& ln, const In& d, float2 (&v)[G1]) const {
+#pragma unroll
+        for (int e = 0; e < G1; ++e) {
+            float2 x = d.f;
+            if constexpr (FEW) {
+                if (e == 0 && (ln.mixed & 1u)) x = d.v[0];
+                if (e == G1 - 1 && ((ln.mixed >> e) & 1u)) x = d.v[1];
+            } else {
+                if ((ln.mixed >> e) & 1u) x = d.v[e];
+            }
+            v[e] = C::bin(ln.rb, e) > C::N / 2 ? make_float2(x.x, -x.y) : x;
+        }
+    }
+    __device__ int64_t out_base(int64_t item) const { return item * C::N; }
+    __device__ void store(int64_t ob, int pos, float2 v) const { out[ob + pos] = v.x * inv_n; }
+};
+
+// Column FFTs (k_cfft_cols's results): item = plane * mw + j is column j of
+// a plane of rows x mw complex values (fft.cpp:111-122, :131-141).  Forward:
+// h rows in, rows < keep (= mh) out.  Inverse: rows < mh in (the rest
+// zero), all h rows out times 1 / h; FEW (mh <= 2^LB): only a lane's
+// element 0 can be a stored row.
+template <int LOG2N, bool INV, bool FEW>
+struct ColIO {
+    using C = FftConsts<LOG2N>;
+    static constexpr int G1 = C::G1;
+    const float2* in;
+    float2* out;
+    const float* tw;
+    int64_t items;
+    int keep;              // forward: mh
+    int mw;
+    int mh;
+    float inv_h;
+    struct Lane { int rb; };
+    struct In { float2 v[INV && FEW ? 1 : G1]; };
+    __device__ Lane lane_setup(int, int rb) const { return Lane{rb}; }
+    // Column item's element (plane * rows + r) * mw + j for r = 0: plane =
+    // item / mw, j = item % mw (items < 2^32, checked at launch).
+    __device__ int64_t col_base(int64_t item, int rows) const {
+        const uint32_t it = static_cast<uint32_t>(item), um = static_cast<uint32_t>(mw);
+        const uint32_t plane = it / um, j = it - plane * um;
+        return static_cast<int64_t>(plane) * rows * mw + j;
+    }
+    __device__ void load(const Lane& ln, int64_t, int64_t item, In& d) const {
+        if (item >= items) {
+#pragma unroll
+            for (int e = 0; e < (INV && FEW ? 1 : G1); ++e) d.v[e] = make_float2(0.0f, 0.0f);
+            return;
+        }
+        const float2* src = in + col_base(item, INV ? mh : C::N);
+        if constexpr (INV && FEW) {
+            d.v[0] = ln.rb < mh ? src[static_cast<int64_t>(ln.rb) * mw] : make_float2(0.0f, 0.0f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < G1; ++e) {
+                const int k = C::bin(ln.rb, e);
+                d.v[e] = (!INV || k < mh) ? src[static_cast<int64_t>(k) * mw] : make_float2(0.0f, 0.0f);
+            }
+        }
+    }
+    __device__ void first(const Lane&, const In& d, float2 (&v)[G1]) const {
+#pragma unroll
+        for (int e = 0; e < G1; ++e) {
+            if constexpr (INV && FEW) v[e] = e == 0 ? d.v[0] : make_float2(0.0f, 0.0f);
+            else v[e] = d.v[e];
+        }
+    }
+    __device__ int64_t out_base(int64_t item) const { return col_base(item, INV ? C::N : mh); }
+    __device__ void store(int64_t ob, int pos, float2 v) const {
+        out[ob + static_cast<int64_t>(pos) * mw] = INV ? make_float2(v.x * inv_h, v.y * inv_h) : v;
+    }
+};
 
 // Column FFT (fft.cpp:48-68 down column j of a plane, fft.cpp:111-122 /
 // :131-141): item = plane * mw + j.
@@ -1493,11 +1643,12 @@ static FftLaunch fft_launch(int64_t items, int n) {
     return f;
 }
 
-// The fixed-length row kernels: lengths 64 .. 1024, a persistent grid of at
-// most eight blocks of four waves per CU, each wave taking R rows at a time.
+// The fixed-length kernels: lengths 64 .. 1024, a persistent grid of at
+// most eight blocks of four waves per CU, each wave taking R sequences at a
+// time.
 template <int LOG2N>
-static bool row_fixed_launch(int64_t items, unsigned& grid, int64_t& nsets, size_t& lds) {
-    if (path_flag(kernel_path().generic_fft)) return false;
+static bool fixed_launch(int64_t items, int keep, unsigned& grid, int64_t& nsets, size_t& lds) {
+    if (path_flag(kernel_path().generic_fft) || keep < 1) return false;
     using F = RowFft<LOG2N>;
     nsets = (items + F::R - 1) / F::R;
     const int64_t blocks = (nsets + 3) / 4, cap = 8 * static_cast<int64_t>(num_cus());
@@ -1506,16 +1657,20 @@ static bool row_fixed_launch(int64_t items, unsigned& grid, int64_t& nsets, size
     return true;
 }
 
+template <int LOG2N, bool PRUNE, bool E0, class IO>
+static void launch_fixed(const IO& io, unsigned grid, int64_t nsets, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((k_fft_fixed<LOG2N, PRUNE, E0, IO>), dim3(grid), dim3(256), lds, st, io, nsets);
+}
+
 template <int LOG2N>
 static bool launch_rfft_fixed(const SpecArgs& a, int64_t items, hipStream_t st) {
     unsigned grid;
     int64_t nsets;
     size_t lds;
-    if (!row_fixed_launch<LOG2N>(items, grid, nsets, lds)) return false;
-    if (a.modes <= RowFft<LOG2N>::G1)
-        hipLaunchKernelGGL((k_rfft_rows_fixed<LOG2N, true>), dim3(grid), dim3(256), lds, st, a, nsets);
-    else
-        hipLaunchKernelGGL((k_rfft_rows_fixed<LOG2N, false>), dim3(grid), dim3(256), lds, st, a, nsets);
+    if (!fixed_launch<LOG2N>(items, a.modes, grid, nsets, lds)) return false;
+    const RowFwdIO<LOG2N> io{a.hc, reinterpret_cast<float2*>(a.spec), a.tw_fwd, items, a.modes};
+    if (a.modes <= RowFft<LOG2N>::G1) launch_fixed<LOG2N, true, true>(io, grid, nsets, lds, st);
+    else launch_fixed<LOG2N, true, false>(io, grid, nsets, lds, st);
     return true;
 }
 
@@ -1524,8 +1679,39 @@ static bool launch_irfft_fixed(const SpecArgs& a, int64_t items, hipStream_t st)
     unsigned grid;
     int64_t nsets;
     size_t lds;
-    if (!row_fixed_launch<LOG2N>(items, grid, nsets, lds)) return false;
-    hipLaunchKernelGGL((k_irfft_rows_fixed<LOG2N>), dim3(grid), dim3(256), lds, st, a, a.spec_mixed, nsets);
+    if (!fixed_launch<LOG2N>(items, a.modes, grid, nsets, lds)) return false;
+    const float2* spec = reinterpret_cast<const float2*>(a.spec_mixed);
+    if (a.modes <= RowFft<LOG2N>::N / RowFft<LOG2N>::G1) {
+        const RowInvIO<LOG2N, true> io{spec, a.x1c, a.fill, a.tw_inv, items, 0, a.modes, a.fill_period, a.inv_n};
+        launch_fixed<LOG2N, false, false>(io, grid, nsets, lds, st);
+    } else {
+        const RowInvIO<LOG2N, false> io{spec, a.x1c, a.fill, a.tw_inv, items, 0, a.modes, a.fill_period, a.inv_n};
+        launch_fixed<LOG2N, false, false>(io, grid, nsets, lds, st);
+    }
+    return true;
+}
+
+template <int LOG2N>
+static bool launch_cfft_fixed(const ColArgs& a, bool inverse, int64_t items, hipStream_t st) {
+    unsigned grid;
+    int64_t nsets;
+    size_t lds;
+    if (items > static_cast<int64_t>(UINT32_MAX) || !fixed_launch<LOG2N>(items, a.mh, grid, nsets, lds)) return false;
+    const float2* in = reinterpret_cast<const float2*>(a.in);
+    float2* out = reinterpret_cast<float2*>(a.out);
+    if (inverse) {
+        if (a.mh <= RowFft<LOG2N>::N / RowFft<LOG2N>::G1) {
+            const ColIO<LOG2N, true, true> io{in, out, a.tw, items, 0, a.mw, a.mh, a.inv_h};
+            launch_fixed<LOG2N, false, false>(io, grid, nsets, lds, st);
+        } else {
+            const ColIO<LOG2N, true, false> io{in, out, a.tw, items, 0, a.mw, a.mh, a.inv_h};
+            launch_fixed<LOG2N, false, false>(io, grid, nsets, lds, st);
+        }
+    } else {
+        const ColIO<LOG2N, false, false> io{in, out, a.tw, items, a.mh, a.mw, a.mh, a.inv_h};
+        if (a.mh <= RowFft<LOG2N>::G1) launch_fixed<LOG2N, true, true>(io, grid, nsets, lds, st);
+        else launch_fixed<LOG2N, true, false>(io, grid, nsets, lds, st);
+    }
     return true;
 }
 
@@ -1552,6 +1738,14 @@ hipError_t launch_rfft_rows(const SpecArgs& a, hipStream_t st) {
 
 hipError_t launch_spec_mix(const SpecArgs& a, hipStream_t st) {
     if (a.samples <= 0 || a.w <= 0 || a.modes <= 0) return hipSuccess;
+    if (a.w <= 64 && a.modes <= 65535 && !path_flag(kernel_path().generic_fft)) {
+        const dim3 mg(static_cast<unsigned>((a.samples + 3) / 4), static_cast<unsigned>(a.modes));
+        if (a.w == 64)
+            hipLaunchKernelGGL(k_spec_mix_lds<64>, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
+        else
+            hipLaunchKernelGGL(k_spec_mix_lds<0>, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
+        return hipGetLastError();
+    }
     const dim3 mg(static_cast<unsigned>((a.samples + 3) / 4), static_cast<unsigned>((a.w + 63) / 64),
                   static_cast<unsigned>(a.modes));
     hipLaunchKernelGGL(k_spec_mix, mg, dim3(256), 0, st, a, a.mix_real, a.mix_imag, a.spec_mixed);
@@ -1588,6 +1782,16 @@ hipError_t launch_spectral(const SpecArgs& a, hipStream_t st) {
 hipError_t launch_cfft_cols(const ColArgs& a, bool inverse, hipStream_t st) {
     const int64_t items = a.planes * a.mw;
     if (items <= 0) return hipSuccess;
+    bool fixed = false;
+    switch (a.log2h) {
+        case 6: fixed = launch_cfft_fixed<6>(a, inverse, items, st); break;
+        case 7: fixed = launch_cfft_fixed<7>(a, inverse, items, st); break;
+        case 8: fixed = launch_cfft_fixed<8>(a, inverse, items, st); break;
+        case 9: fixed = launch_cfft_fixed<9>(a, inverse, items, st); break;
+        case 10: fixed = launch_cfft_fixed<10>(a, inverse, items, st); break;
+        default: break;
+    }
+    if (fixed) return hipGetLastError();
     const FftLaunch f = fft_launch(items, a.h);
     if (inverse) {
         if (f.small)

@@ -72,6 +72,8 @@ CASES = [
     (1, 1024, 1, 1, 8, 100, 1, 1, False, None, False),
     (3, 64, 1, 1, 5, 4, 1, 1, False, None, False),
     (3, 64, 1, 1, 5, 33, 1, 1, True, None, False),
+    (2, 128, 1, 1, 8, 6, 1, 1, False, None, False),
+    (1, 512, 1, 1, 4, 80, 1, 1, True, None, False),
 ]
 
 

@@ -54,6 +54,12 @@ CASES = [
     # part-filled row set of 8 at 128 points).
     (1, 4, 128, 1, 1, 3, 3, 20, 1, 1, False, ["tensor"]),
     (2, 4, 512, 1, 1, 4, 2, 6, 1, 1, True, None),
+    # Column lengths 256 (mh above 16: every group of the forward's later
+    # passes and every stored row of the inverse), 512 and 1024 on the
+    # fixed-length column FFTs.
+    (1, 256, 8, 1, 1, 4, 20, 3, 1, 1, False, None),
+    (1, 512, 4, 1, 1, 4, 6, 2, 1, 1, True, None),
+    (1, 1024, 2, 1, 1, 4, 70, 2, 1, 1, False, ["tensor"]),
     (2, 8, 8, 1, 1, 8, 8, 5, 1, 1, False, None),            # all H rows and all W/2 + 1 bins
     (1, 4, 2, 1, 1, 4, 2, 2, 0, 1, False, ["tensor"]),       # no layers
     # Output element counts that are not a multiple of 4 (the fake-quant
@@ -85,6 +91,31 @@ def test_run_bit_exact(gpu, tmp_path, case):
     assert np.array_equal(_bits(y), _bits(want)), int((_bits(y) != _bits(want)).sum())
     if REF_RUN.exists() and x.size * case[5] <= 1 << 20:
         assert np.array_equal(_bits(y), _bits(ref_run(tmp_path, ir, x, case[4])))
+
+
+@pytest.mark.parametrize("case", [(2, 64, 64, 1, 1, 16, 12, 12, 2, 1, False, ["fp8"]),
+                                  (1, 256, 8, 1, 1, 4, 20, 3, 1, 1, True, None)], ids=_ids)
+def test_fixed_size_kernels_equal_generic(gpu, tmp_path, case):
+    """The fixed-length row and column FFTs and the LDS-staged channel mix
+    against the any-size kernels (kernel path generic_fft) and the oracle."""
+    import ctypes as C
+    ncpp = load()
+    ir, x, m = _model(case)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    want = OF2.forward(m, x)
+    L = _lib.lib()
+    b, H, W, _ = x.shape
+    for flag in (0, 1):
+        prev = C.c_int(0)
+        _lib.check(L.nflow_debug_set_kernel_path(b"generic_fft", flag, C.byref(prev)), "kernel path")
+        try:
+            rt = ncpp.InferenceRuntime(str(path))
+            y = np.zeros((b, H, W, case[4]), np.float32)
+            rt.run(x, y)
+        finally:
+            _lib.check(L.nflow_debug_set_kernel_path(b"generic_fft", prev.value, None), "kernel path")
+        assert np.array_equal(_bits(y), _bits(want)), (flag, int((_bits(y) != _bits(want)).sum()))
 
 
 def test_run_device_and_infer_arrays(gpu, tmp_path):
