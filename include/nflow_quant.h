@@ -108,7 +108,8 @@ const char* nflow_last_error(void);
  * persistent GEMM), "no_rows64_queue" (0 / 1: the K = N = 64 layer with
  * its static tile deal instead of the per-CU tile queue) and
  * "no_layer_tail" (0 / 1: the FNO runtime's width-64 local-linear layer and
- * its tail as two launches instead of one) and "generic_fft" (0 / 1: the
+ * its tail as two launches instead of one, and its projection head as two
+ * to four instead of one) and "generic_fft" (0 / 1: the
  * FNO runtime's row FFTs of 64 .. 1024 points and its channel mix of up to
  * 64 channels on the any-size kernels instead of the fixed-size ones).  The
  * environment variables NFLOW_<NAME> set the initial values, read once at

@@ -176,6 +176,30 @@ bool layer_tail_ok(const PostArgs& p, int in_features, int out_features);
 // one pass, on the same conditions; W (64, 64) and b (64 or null) fp32.
 bool linear_tail_ok(const PostArgs& p, const float* W);
 hipError_t launch_linear_tail(const PostArgs& a, const float* W, const float* b, hipStream_t st);
+
+// The projection head (fno.cpp:662-698, :966-993) in one pass: y = fq_o(
+// proj_out(act(fq_q(proj_q(h))))) for width 64 and one output channel, with
+// the sums and forms of launch_linear_ref and launch_fq_act.  h is
+// token-major with rows_in rows per sample, of which the first n are read;
+// y is (samples, n).
+struct ProjArgs {
+    const float* h;
+    float* y;
+    const float* Wq;
+    const float* bq;
+    const float* Wo;
+    const float* bo;
+    int64_t samples;
+    int n;
+    int rows_in;
+    int w;
+    int out_ch;
+    int act;
+    FakeQuant fq_q;
+    FakeQuant fq_o;
+};
+bool proj_tail_ok(const ProjArgs& p);
+hipError_t launch_proj_tail(const ProjArgs& a, hipStream_t st);
 // The device arrays of an INT8 layer handle into a (layer.cpp): false for
 // another format.
 bool layer_int8_arrays(const nflow_layer* layer, LayerTailArgs* a, int* in_features, int* out_features);

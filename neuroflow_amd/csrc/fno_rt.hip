@@ -922,22 +922,32 @@ __device__ __forceinline__ const float2* stage_row_twiddles(float2* smem, const 
     return smem;
 }
 
-// The persistent row-set loop: a wave loads the inputs of its next set into
-// one of two register buffers while it transforms the set held in the other
-// (the two alternate, so no copy between them).
-template <typename Buf, typename Load, typename Run>
-__device__ __forceinline__ void row_sets(int64_t first, int64_t stride, int64_t nsets, Buf& b0, Buf& b1,
+// The persistent row-set loop: a wave loads the inputs of the set NB - 1
+// ahead into one of NB register buffers while it transforms the set held in
+// another (the buffers rotate, so no copy between them).  Every load is
+// issued whether its set exists or not (past the end, the last set's rows
+// are read again and dropped): loads under no branch let the compiler wait
+// for one buffer's loads only, with the others' still in flight.
+template <int NB, typename Buf, typename Load, typename Run>
+__device__ __forceinline__ void row_sets(int64_t first, int64_t stride, int64_t nsets, Buf (&b)[NB],
                                          const Load& load, const Run& run) {
+    const int64_t last = nsets - 1;
     int64_t set = first;
-    if (set < nsets) load(set, b0);
+#pragma unroll
+    for (int i = 0; i < NB - 1; ++i) {
+        const int64_t s = set + i * stride;
+        load(s < last ? s : last, b[i]);
+    }
     while (set < nsets) {
-        if (set + stride < nsets) load(set + stride, b1);
-        run(set, b0);
-        set += stride;
-        if (set >= nsets) break;
-        if (set + stride < nsets) load(set + stride, b0);
-        run(set, b1);
-        set += stride;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int64_t pre = set + (NB - 1) * stride;
+            load(pre < last ? pre : last, b[(i + NB - 1) % NB]);
+            __builtin_amdgcn_sched_barrier(0);   // the loads go out before the transform
+            run(set, b[i]);
+            set += stride;
+            if (set >= nsets) break;
+        }
     }
 }
 
@@ -947,7 +957,8 @@ __device__ __forceinline__ void row_sets(int64_t first, int64_t stride, int64_t 
 // IO::In, one set's prefetched inputs; load(lane, set, item, in);
 // first(lane, in, v), the first pass's G1 inputs (element e = input
 // bitrev(g G1 + e) = bitrev_P1(e) 2^LB + bitrev_LB(g)); out_base(item) and
-// store(base, position, value) for the kept outputs.
+// store(base, position, value) for the kept outputs; DEPTH, the sets in
+// flight (loaded DEPTH - 1 ahead).
 template <int LOG2N, bool PRUNE, bool E0, class IO>
 __global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
     using F = RowFft<LOG2N>;
@@ -963,15 +974,15 @@ __global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
     auto load = [&](int64_t set, In& d) { io.load(ln, set, set * R + row1, d); };
     auto run = [&](int64_t set, const In& d) {
         float2 v[G1];
-        io.first(ln, d, v);
+        io.first(ln, d, v, reinterpret_cast<float*>(buf), lane);
         row_stages<RowFftPlan<LOG2N>::P1, 1>(v, tw, 0);
 #pragma unroll
         for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
         row_rest<LOG2N, PRUNE, E0>(buf, tw, lane, set * R, io);
     };
-    In b0{}, b1{};
-    row_sets(static_cast<int64_t>(blockIdx.x) * 4 + wid, static_cast<int64_t>(gridDim.x) * 4, nsets, b0, b1, load,
-             run);
+    In b[IO::DEPTH];
+    row_sets<IO::DEPTH>(static_cast<int64_t>(blockIdx.x) * 4 + wid, static_cast<int64_t>(gridDim.x) * 4, nsets, b,
+                        load, run);
 }
 
 template <int LOG2N> struct FftConsts {
@@ -984,27 +995,48 @@ template <int LOG2N> struct FftConsts {
 template <int LOG2N>
 struct RowFwdIO {
     using C = FftConsts<LOG2N>;
+    static constexpr int DEPTH = 3;
     const float* hc;
     float2* spec;
     const float* tw;
     int64_t items;
     int keep;
-    struct Lane { int rb; };
+    struct Lane { int rb, row, c; };
     struct In { float v[C::G1]; };
-    __device__ Lane lane_setup(int, int rb) const { return Lane{rb}; }
+    __device__ Lane lane_setup(int row1, int rb) const {
+        // The natural-order load role: row1, and the lane's 16-byte column
+        // within the row's first-pass lanes.
+        return Lane{rb, row1, static_cast<int>(threadIdx.x & 63) % (C::N / C::G1)};
+    }
+    // The row is read in natural order, 16 bytes a lane (lane (r, c) of the
+    // set's row r takes floats 64 q + 4 c .. + 3, q < G1 / 4: whole 256-byte
+    // runs per instruction), and put in first-pass order through the wave's
+    // buffer (rows RS floats apart, so that the four rows' gathers fall on
+    // distinct banks).
+    static constexpr int Q = C::G1 / 4, RS = C::N + 16;
+    static_assert(C::G1 % 4 == 0 && RowFft<LOG2N>::R * RS <= 2 * RowFft<LOG2N>::WAVE_SLOTS, "row scratch");
     __device__ void load(const Lane& ln, int64_t, int64_t item, In& d) const {
-        if (item < items) {
-            const float* src = hc + item * C::N + ln.rb;
+        // A row past the end reads the last row: transformed, never stored.
+        const v4f* src = reinterpret_cast<const v4f*>(hc + (item < items ? item : items - 1) * C::N) + ln.c;
 #pragma unroll
-            for (int e = 0; e < C::G1; ++e) d.v[e] = src[bitrevc(e, C::P1) << C::LB];
-        } else {
-#pragma unroll
-            for (int e = 0; e < C::G1; ++e) d.v[e] = 0.0f;    // a row past the end: transformed, never stored
+        for (int q = 0; q < Q; ++q) {
+            const v4f x = src[q * (C::N / 4 / Q)];
+            d.v[4 * q] = x[0];
+            d.v[4 * q + 1] = x[1];
+            d.v[4 * q + 2] = x[2];
+            d.v[4 * q + 3] = x[3];
         }
     }
-    __device__ void first(const Lane&, const In& d, float2 (&v)[C::G1]) const {
+    __device__ void first(const Lane& ln, const In& d, float2 (&v)[C::G1], float* scratch, int) const {
+        float* row = scratch + ln.row * RS;
 #pragma unroll
-        for (int e = 0; e < C::G1; ++e) v[e] = make_float2(d.v[e], 0.0f);
+        for (int q = 0; q < Q; ++q)
+            *reinterpret_cast<v4f*>(row + q * (C::N / Q) + 4 * ln.c) =
+                v4f{d.v[4 * q], d.v[4 * q + 1], d.v[4 * q + 2], d.v[4 * q + 3]};
+        wave_sync();
+#pragma unroll
+        for (int e = 0; e < C::G1; ++e) v[e] = make_float2(row[C::bin(ln.rb, e)], 0.0f);
+        wave_sync();
     }
     __device__ int64_t out_base(int64_t item) const { return item * keep; }
     __device__ void store(int64_t ob, int pos, float2 v) const { spec[ob + pos] = v; }
@@ -1017,7 +1049,7 @@ struct RowFwdIO {
 template <int LOG2N, bool FEW>
 struct RowInvIO {
     using C = FftConsts<LOG2N>;
-    static constexpr int G1 = C::G1;
+    static constexpr int G1 = C::G1, DEPTH = 2;
     const float2* spec;
     float* out;
     const float2* fill;
@@ -1062,7 +1094,7 @@ struct RowInvIO {
                 if ((ln.mixed >> e) & 1u) d.v[e] = *reinterpret_cast<const float2*>(src + ln.off[e]);
         }
     }
-    __device__ void first(const Lane& ln, const In& d, float2 (&v)[G1]) const {
+    __device__ void first(const Lane& ln, const In& d, float2 (&v)[G1], float*, int) const {
 #pragma unroll
         for (int e = 0; e < G1; ++e) {
             float2 x = d.f;
@@ -1087,7 +1119,7 @@ struct RowInvIO {
 template <int LOG2N, bool INV, bool FEW>
 struct ColIO {
     using C = FftConsts<LOG2N>;
-    static constexpr int G1 = C::G1;
+    static constexpr int G1 = C::G1, DEPTH = 2;
     const float2* in;
     float2* out;
     const float* tw;
@@ -1107,12 +1139,8 @@ struct ColIO {
         return static_cast<int64_t>(plane) * rows * mw + j;
     }
     __device__ void load(const Lane& ln, int64_t, int64_t item, In& d) const {
-        if (item >= items) {
-#pragma unroll
-            for (int e = 0; e < (INV && FEW ? 1 : G1); ++e) d.v[e] = make_float2(0.0f, 0.0f);
-            return;
-        }
-        const float2* src = in + col_base(item, INV ? mh : C::N);
+        // A column past the end reads the last column: transformed, never stored.
+        const float2* src = in + col_base(item < items ? item : items - 1, INV ? mh : C::N);
         if constexpr (INV && FEW) {
             d.v[0] = ln.rb < mh ? src[static_cast<int64_t>(ln.rb) * mw] : make_float2(0.0f, 0.0f);
         } else {
@@ -1123,7 +1151,7 @@ struct ColIO {
             }
         }
     }
-    __device__ void first(const Lane&, const In& d, float2 (&v)[G1]) const {
+    __device__ void first(const Lane&, const In& d, float2 (&v)[G1], float*, int) const {
 #pragma unroll
         for (int e = 0; e < G1; ++e) {
             if constexpr (INV && FEW) v[e] = e == 0 ? d.v[0] : make_float2(0.0f, 0.0f);
@@ -1478,6 +1506,78 @@ __global__ __launch_bounds__(256) void k_linear_tail(PostArgs a, const float* Wl
 #pragma unroll
         for (int q = 0; q < PER; ++q) a.hc[cb + q * d1] = tx1[cm + CSTEP * q][tm];
         __syncthreads();
+    }
+}
+
+// The projection head in one pass (fno.cpp:662-698, :966-993): proj_q
+// (64 -> 64, k_linear_rows64's sums), its fake-quant FQQ and the activation,
+// then proj_out (64 -> 1, k_linear_narrow64's sums over the 64 activations
+// in order) and its fake-quant FQO, on 32-token tiles.  Lane j of each wave
+// holds row j of proj_q.weight in registers; the h tile and the activations
+// are staged in LDS (token-major), and 32 threads take one token's proj_out
+// each.
+template <int ACT, int FQQ, int FQO>
+__global__ __launch_bounds__(256) void k_proj_tail(ProjArgs a) {
+    constexpr int TT = 32, HS = 68, QS = 65, PER = TT * 64 / 256;
+    __shared__ __attribute__((aligned(16))) float th[TT * HS];
+    __shared__ float tq[TT * QS];
+    __shared__ float wo_s[64];
+    __shared__ float steps_q[16], steps_o[16];
+    if (threadIdx.x < 64) wo_s[threadIdx.x] = a.Wo[threadIdx.x];
+    stage_steps(steps_q, a.fq_q.thr);
+    stage_steps(steps_o, a.fq_o.thr);
+    const ScaleInv inv_q = scale_inv(a.fq_q.scale), inv_o = scale_inv(a.fq_o.scale);
+    const int tk = threadIdx.x / 64, ck = threadIdx.x % 64;
+    const int hq_t = threadIdx.x / 16, hq_c = 4 * (threadIdx.x % 16);
+    float wr[64];
+#pragma unroll
+    for (int p = 0; p < 64; p += 4) {
+        const v4f q = *reinterpret_cast<const v4f*>(a.Wq + ck * 64 + p);
+        wr[p] = q[0];
+        wr[p + 1] = q[1];
+        wr[p + 2] = q[2];
+        wr[p + 3] = q[3];
+    }
+    const float bj = a.bq ? a.bq[ck] : 0.0f;
+    const float bo = a.bo ? a.bo[0] : 0.0f;
+    const int n = a.n;
+    Tile tl;
+    for (int64_t id = blockIdx.x; tile_of<TT>(id, a.samples, n, 64, tl); id += gridDim.x) {
+        const float* hs = a.h + (tl.s * a.rows_in + tl.t0) * 64;
+        v4f hv[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) hv[q] = *reinterpret_cast<const v4f*>(hs + (hq_t + 16 * q) * 64 + hq_c);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) *reinterpret_cast<v4f*>(th + (hq_t + 16 * q) * HS + hq_c) = hv[q];
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const float* hr = th + (tk + 4 * q) * HS;
+            float acc = bj;
+#pragma unroll
+            for (int p = 0; p < 64; p += 4) {
+                const v4f x = *reinterpret_cast<const v4f*>(hr + p);
+                acc = acc + x[0] * wr[p];
+                acc = acc + x[1] * wr[p + 1];
+                acc = acc + x[2] * wr[p + 2];
+                acc = acc + x[3] * wr[p + 3];
+            }
+            if constexpr (FQQ == 1) acc = x2_fake_quant_inv(acc, a.fq_q.scale, inv_q.inv, inv_q.ok, a.fq_q.zpf);
+            else if constexpr (FQQ == 3) acc = log2_snap(acc, a.fq_q.scale, steps_q);
+            if constexpr (ACT == RT_ACT_RELU) acc = acc < 0.0f ? 0.0f : acc;   // fno.cpp:37-40
+            else if constexpr (ACT == RT_ACT_GELU) acc = gelu_fast<kGeluRefine>(acc);
+            tq[(tk + 4 * q) * QS + ck] = acc;
+        }
+        __syncthreads();
+        if (threadIdx.x < TT) {
+            const float* qr = tq + threadIdx.x * QS;
+            float acc = bo;
+#pragma unroll
+            for (int j = 0; j < 64; ++j) acc = acc + qr[j] * wo_s[j];
+            if constexpr (FQO == 1) acc = x2_fake_quant_inv(acc, a.fq_o.scale, inv_o.inv, inv_o.ok, a.fq_o.zpf);
+            else if constexpr (FQO == 3) acc = log2_snap(acc, a.fq_o.scale, steps_o);
+            a.y[tl.s * n + tl.t0 + threadIdx.x] = acc;
+        }
     }
 }
 
@@ -1944,6 +2044,40 @@ hipError_t launch_linear_tail(const PostArgs& a, const float* W, const float* b,
         case 3: launch_linear_tail_act<3>(a, W, b, grid, st); break;
         default: launch_linear_tail_act<0>(a, W, b, grid, st); break;
     }
+    return hipGetLastError();
+}
+
+// The projection head in one launch: proj_q 64 -> 64 and proj_out 64 -> 1,
+// whole 32-token tiles, at least two tiles per CU, the fake-quant forms off /
+// per tensor / log2 snap, 16-byte aligned h rows and proj_q weight.
+bool proj_tail_ok(const ProjArgs& p) {
+    const auto fq_ok = [](const FakeQuant& f) { return f.on == 0 || f.on == 1 || f.on == 3; };
+    return !path_flag(kernel_path().no_layer_tail) && p.w == 64 && p.out_ch == 1 && p.n > 0 && p.n % 32 == 0 &&
+           p.rows_in >= p.n && tile_count(p.samples, p.n, 64, 32) >= 2 * static_cast<int64_t>(num_cus()) &&
+           fq_ok(p.fq_q) && fq_ok(p.fq_o) && (p.act == RT_ACT_NONE || p.act == RT_ACT_RELU || p.act == RT_ACT_GELU) &&
+           aligned(p.h, 16) && aligned(p.Wq, 16);
+}
+
+template <int ACT, int FQQ>
+static void launch_proj_tail_fqo(const ProjArgs& a, unsigned grid, hipStream_t st) {
+    if (a.fq_o.on == 1) hipLaunchKernelGGL((k_proj_tail<ACT, FQQ, 1>), dim3(grid), dim3(256), 0, st, a);
+    else if (a.fq_o.on == 3) hipLaunchKernelGGL((k_proj_tail<ACT, FQQ, 3>), dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_proj_tail<ACT, FQQ, 0>), dim3(grid), dim3(256), 0, st, a);
+}
+
+template <int ACT>
+static void launch_proj_tail_fqq(const ProjArgs& a, unsigned grid, hipStream_t st) {
+    if (a.fq_q.on == 1) launch_proj_tail_fqo<ACT, 1>(a, grid, st);
+    else if (a.fq_q.on == 3) launch_proj_tail_fqo<ACT, 3>(a, grid, st);
+    else launch_proj_tail_fqo<ACT, 0>(a, grid, st);
+}
+
+hipError_t launch_proj_tail(const ProjArgs& a, hipStream_t st) {
+    if (a.samples <= 0) return hipSuccess;
+    const unsigned grid = grid_for(tile_count(a.samples, a.n, 64, 32), 1, 8);
+    if (a.act == RT_ACT_GELU) launch_proj_tail_fqq<RT_ACT_GELU>(a, grid, st);
+    else if (a.act == RT_ACT_RELU) launch_proj_tail_fqq<RT_ACT_RELU>(a, grid, st);
+    else launch_proj_tail_fqq<RT_ACT_NONE>(a, grid, st);
     return hipGetLastError();
 }
 

@@ -57,7 +57,7 @@ struct KernelPath {
     std::atomic<int> gemm_mfma{0};   // 0: the launcher's choice, else 16 or 32
     std::atomic<int> no_wide{0};
     std::atomic<int> no_rows64_queue{0};
-    std::atomic<int> no_layer_tail{0};   // the FNO runtime's INT8 layer + tail as two launches
+    std::atomic<int> no_layer_tail{0};   // the FNO runtime's layer + tail and projection head unfused
     std::atomic<int> generic_fft{0};     // the FNO runtime's row FFTs and channel mix on the any-size kernels
 };
 KernelPath& kernel_path();

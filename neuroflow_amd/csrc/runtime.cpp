@@ -682,7 +682,12 @@ int run_device(nflow_runtime* rt, const float* x, const int64_t* xs, float* y, h
         }
         if (int rc = launch_check(launch_post(pa, st), "layer tail")) return rc;
     }
-    // Trim, proj_q + act, proj_out (fno.cpp:662-698).
+    // Trim, proj_q + act, proj_out (fno.cpp:662-698): one launch where it
+    // applies (the same bits as the two below).
+    ProjArgs pj{H, y, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), rt->dw("proj_out.weight"),
+                rt->dw("proj_out.bias"), b, static_cast<int>(n), static_cast<int>(n_pad), w, rt->out_ch, rt->act,
+                FakeQuant{}, FakeQuant{}};
+    if (proj_tail_ok(pj)) return launch_check(launch_proj_tail(pj, st), "projection");
     LinArgs pq{H, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X2, b, static_cast<int>(n), static_cast<int>(n),
                static_cast<int>(n_pad), w, w, rt->act};
     if (int rc = launch_check(launch_linear_ref(pq, st), "proj_q")) return rc;
@@ -859,6 +864,9 @@ int run_device_2d(nflow_runtime* rt, const float* x, const int64_t* xs, float* y
         if (int rc = launch_check(launch_pad2d(Hb, P, b, H, W, Hp, Wp, w, true, st), "trim")) return rc;
         hsrc = P;
     }
+    ProjArgs pj{hsrc, y, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), rt->dw("proj_out.weight"),
+                rt->dw("proj_out.bias"), b, ip0, ip0, w, rt->out_ch, rt->act, rt->fq_projq, rt->fq_projout};
+    if (proj_tail_ok(pj)) return launch_check(launch_proj_tail(pj, st), "projection");
     const bool pq_fq = rt->fq_projq.on != 0;
     LinArgs pq{hsrc, rt->dw("proj_q.weight"), rt->dw("proj_q.bias"), X2, b, ip0, ip0, ip0, w, w,
                pq_fq ? static_cast<int>(RT_ACT_NONE) : rt->act};

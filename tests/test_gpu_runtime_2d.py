@@ -118,6 +118,35 @@ def test_fixed_size_kernels_equal_generic(gpu, tmp_path, case):
         assert np.array_equal(_bits(y), _bits(want)), (flag, int((_bits(y) != _bits(want)).sum()))
 
 
+@pytest.mark.parametrize("relu,kinds", [(False, ["tensor", "fp8"]), (True, ["fp8", "tensor"]),
+                                        (False, ["fp8zero", "tensor", "fp8"]), (False, None)])
+def test_fused_launches_equal_separate(gpu, tmp_path, relu, kinds):
+    """The width-64 local linear + tail (k_linear_tail) and the projection
+    head (k_proj_tail) in one launch each against their separate launches
+    (kernel path no_layer_tail) and the oracle, with proj_q / proj_out
+    fake-quants off, per tensor, log2 snap and disabled by an FP8 record of
+    scale 0."""
+    import ctypes as C
+    case = (4, 64, 64, 1, 1, 64, 12, 12, 2, 1, relu, kinds)
+    ncpp = load()
+    ir, x, m = _model(case)
+    path = tmp_path / "m.nneuroir"
+    path.write_bytes(ir)
+    want = OF2.forward(m, x)
+    L = _lib.lib()
+    b, H, W, _ = x.shape
+    for flag in (0, 1):
+        prev = C.c_int(0)
+        _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", flag, C.byref(prev)), "kernel path")
+        try:
+            rt = ncpp.InferenceRuntime(str(path))
+            y = np.zeros((b, H, W, 1), np.float32)
+            rt.run(x, y)
+        finally:
+            _lib.check(L.nflow_debug_set_kernel_path(b"no_layer_tail", prev.value, None), "kernel path")
+        assert np.array_equal(_bits(y), _bits(want)), (flag, int((_bits(y) != _bits(want)).sum()))
+
+
 def test_run_device_and_infer_arrays(gpu, tmp_path):
     import torch
     ncpp = load()
