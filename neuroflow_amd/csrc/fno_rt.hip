@@ -1743,17 +1743,18 @@ static FftLaunch fft_launch(int64_t items, int n) {
     return f;
 }
 
-// The fixed-length kernels: lengths 64 .. 1024, a persistent grid of at
-// most eight blocks of four waves per CU, each wave taking R sequences at a
-// time.
+// The fixed-length kernels: lengths 64 .. 1024, a persistent grid of as
+// many blocks of four waves as the CUs' LDS holds at once (160 KiB each),
+// each wave taking R sequences at a time.
 template <int LOG2N>
 static bool fixed_launch(int64_t items, int keep, unsigned& grid, int64_t& nsets, size_t& lds) {
     if (path_flag(kernel_path().generic_fft) || keep < 1) return false;
     using F = RowFft<LOG2N>;
     nsets = (items + F::R - 1) / F::R;
-    const int64_t blocks = (nsets + 3) / 4, cap = 8 * static_cast<int64_t>(num_cus());
-    grid = static_cast<unsigned>(blocks < cap ? blocks : cap);
     lds = (static_cast<size_t>(F::N) + 4 * static_cast<size_t>(F::WAVE_SLOTS)) * sizeof(float2);
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / static_cast<int64_t>(lds)));
+    const int64_t blocks = (nsets + 3) / 4, cap = per_cu * static_cast<int64_t>(num_cus());
+    grid = static_cast<unsigned>(blocks < cap ? blocks : cap);
     return true;
 }
 
