@@ -980,7 +980,7 @@ __global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
         for (int e = 0; e < G1; ++e) buf[F::slot(row1, g1 * G1 + e)] = v[e];
         row_rest<LOG2N, PRUNE, E0>(buf, tw, lane, set * R, io);
     };
-    In b[IO::DEPTH];
+    In b[IO::DEPTH] = {};
     row_sets<IO::DEPTH>(static_cast<int64_t>(blockIdx.x) * 4 + wid, static_cast<int64_t>(gridDim.x) * 4, nsets, b,
                         load, run);
 }
