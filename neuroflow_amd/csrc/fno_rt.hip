@@ -817,11 +817,11 @@ __global__ __launch_bounds__(64 * WPB) void k_irfft(SpecArgs a, const float* spe
 // conflicts at n = 256).
 // ---------------------------------------------------------------------------
 template <int LOG2N> struct RowFftPlan;
-template <> struct RowFftPlan<6> { static constexpr int P1 = 3, P2 = 3, P3 = 0, SL = 3, STRIDE = 72; };
-template <> struct RowFftPlan<7> { static constexpr int P1 = 4, P2 = 3, P3 = 0, SL = 4, STRIDE = 136; };
-template <> struct RowFftPlan<8> { static constexpr int P1 = 4, P2 = 4, P3 = 0, SL = 4, STRIDE = 272; };
-template <> struct RowFftPlan<9> { static constexpr int P1 = 3, P2 = 3, P3 = 3, SL = 3, STRIDE = 576; };
-template <> struct RowFftPlan<10> { static constexpr int P1 = 4, P2 = 3, P3 = 3, SL = 4, STRIDE = 1088; };
+template <> struct RowFftPlan<6> { static constexpr int P1 = 3, P2 = 3, P3 = 0, SL = 3, STRIDE = 72, WPB = 4; };
+template <> struct RowFftPlan<7> { static constexpr int P1 = 4, P2 = 3, P3 = 0, SL = 4, STRIDE = 136, WPB = 4; };
+template <> struct RowFftPlan<8> { static constexpr int P1 = 4, P2 = 4, P3 = 0, SL = 4, STRIDE = 272, WPB = 4; };
+template <> struct RowFftPlan<9> { static constexpr int P1 = 3, P2 = 3, P3 = 3, SL = 3, STRIDE = 576, WPB = 8; };
+template <> struct RowFftPlan<10> { static constexpr int P1 = 4, P2 = 3, P3 = 3, SL = 4, STRIDE = 1088, WPB = 8; };
 
 template <int LOG2N>
 struct RowFft {
@@ -960,7 +960,7 @@ __device__ __forceinline__ void row_sets(int64_t first, int64_t stride, int64_t 
 // store(base, position, value) for the kept outputs; DEPTH, the sets in
 // flight (loaded DEPTH - 1 ahead).
 template <int LOG2N, bool PRUNE, bool E0, class IO>
-__global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
+__global__ __launch_bounds__(64 * RowFftPlan<LOG2N>::WPB) void k_fft_fixed(IO io, int64_t nsets) {
     using F = RowFft<LOG2N>;
     constexpr int N = F::N, G1 = F::G1, R = F::R, GPR1 = N / G1, LB = LOG2N - RowFftPlan<LOG2N>::P1;
     extern __shared__ float2 fsm[];
@@ -981,7 +981,8 @@ __global__ __launch_bounds__(256) void k_fft_fixed(IO io, int64_t nsets) {
         row_rest<LOG2N, PRUNE, E0>(buf, tw, lane, set * R, io);
     };
     In b[IO::DEPTH] = {};
-    row_sets<IO::DEPTH>(static_cast<int64_t>(blockIdx.x) * 4 + wid, static_cast<int64_t>(gridDim.x) * 4, nsets, b,
+    constexpr int WPB = RowFftPlan<LOG2N>::WPB;
+    row_sets<IO::DEPTH>(static_cast<int64_t>(blockIdx.x) * WPB + wid, static_cast<int64_t>(gridDim.x) * WPB, nsets, b,
                         load, run);
 }
 
@@ -995,7 +996,7 @@ template <int LOG2N> struct FftConsts {
 template <int LOG2N>
 struct RowFwdIO {
     using C = FftConsts<LOG2N>;
-    static constexpr int DEPTH = 3;
+    static constexpr int DEPTH = 2;
     const float* hc;
     float2* spec;
     const float* tw;
@@ -1744,23 +1745,26 @@ static FftLaunch fft_launch(int64_t items, int n) {
 }
 
 // The fixed-length kernels: lengths 64 .. 1024, a persistent grid of as
-// many blocks of four waves as the CUs' LDS holds at once (160 KiB each),
-// each wave taking R sequences at a time.
+// many blocks as the CUs' LDS holds at once (160 KiB each; blocks of WPB
+// waves sharing one twiddle table: 8 at 512 and 1024 points, whose tables
+// are the largest), each wave taking R sequences at a time.
 template <int LOG2N>
 static bool fixed_launch(int64_t items, int keep, unsigned& grid, int64_t& nsets, size_t& lds) {
     if (path_flag(kernel_path().generic_fft) || keep < 1) return false;
     using F = RowFft<LOG2N>;
     nsets = (items + F::R - 1) / F::R;
-    lds = (static_cast<size_t>(F::N) + 4 * static_cast<size_t>(F::WAVE_SLOTS)) * sizeof(float2);
+    constexpr int WPB = RowFftPlan<LOG2N>::WPB;
+    lds = (static_cast<size_t>(F::N) + WPB * static_cast<size_t>(F::WAVE_SLOTS)) * sizeof(float2);
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(8, (160 * 1024) / static_cast<int64_t>(lds)));
-    const int64_t blocks = (nsets + 3) / 4, cap = per_cu * static_cast<int64_t>(num_cus());
+    const int64_t blocks = (nsets + WPB - 1) / WPB, cap = per_cu * static_cast<int64_t>(num_cus());
     grid = static_cast<unsigned>(blocks < cap ? blocks : cap);
     return true;
 }
 
 template <int LOG2N, bool PRUNE, bool E0, class IO>
 static void launch_fixed(const IO& io, unsigned grid, int64_t nsets, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((k_fft_fixed<LOG2N, PRUNE, E0, IO>), dim3(grid), dim3(256), lds, st, io, nsets);
+    hipLaunchKernelGGL((k_fft_fixed<LOG2N, PRUNE, E0, IO>), dim3(grid), dim3(64 * RowFftPlan<LOG2N>::WPB), lds, st, io,
+                       nsets);
 }
 
 template <int LOG2N>
